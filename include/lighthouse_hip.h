@@ -1,0 +1,180 @@
+/*
+ * lighthouse_hip.h - C ABI of the gfx950 Lighthouse selection-attention library
+ * (liblighthouse_hip.so).
+ *
+ * Every entry point:
+ *   - takes plain device pointers, sizes and element strides (no framework types);
+ *   - launches asynchronously on `stream` (a hipStream_t passed as void*; NULL =
+ *     the default stream) and never synchronizes the host;
+ *   - allocates no memory: every buffer is owned by the caller;
+ *   - returns LH_OK (0) or an LH_ERR_* code (lh_strerror() names it); argument
+ *     errors are detected on the host before any launch.
+ *
+ * Layouts (B batch, S base length, H heads, D = 128 head dim, p pooling
+ * factor, L levels, S_tot = sum_l S/p^(l-1), Sp = S_tot - S, n = selected
+ * length):
+ *   base rows     bf16 [B, S, H, D]   (the model's xq/xk/xv, post-RoPE)
+ *   pooled rows   bf16 [B, Sp, H, D]  (levels 2..L, base-first order)
+ *   scores        fp32 [B, H, S_tot]  (bf16-rounded norms, widened)
+ *   indices       int32 [B, H, n]     pyramid indices in causal order
+ *   inverse       int32 [B, H, S_tot] position in the selected sequence or -1
+ *   selected rows bf16 [B, H, n, D];  lse / delta fp32 [B, H, n]
+ *   layer output  bf16 [B, H, S, D]
+ *
+ * Citations are to the reference repository (ighoshsubho/lighthouse-attention).
+ */
+#ifndef LIGHTHOUSE_HIP_H
+#define LIGHTHOUSE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LH_OK 0
+#define LH_ERR_INVALID_ARG 1  /* bad size, null pointer or unsupported shape */
+#define LH_ERR_DOMAIN 2       /* geometry the reference asserts on or overruns (strict mode) */
+#define LH_ERR_LAUNCH 3       /* the HIP runtime refused a launch */
+#define LH_ERR_UNSUPPORTED 4  /* shape beyond this build's limits (e.g. D != 128) */
+
+#define LH_TIE_REFERENCE 0    /* the reference network: strict compare-exchange only */
+#define LH_TIE_LOWER_INDEX 1  /* ties ordered by lower level-local index */
+
+/* Human-readable name of a return code. */
+const char *lh_strerror(int rc);
+
+/* ABI version of this header (bumped on any signature change). */
+int lh_abi_version(void);
+
+/*
+ * Tiling of the selection and the selected length.
+ * Replaces compute_output_indices_selection (src/lighthouse_selection_cuda.py:346-357)
+ * and the tiling/asserts of LighthouseSelectionQkKqChunkedTopkNvrtc.forward
+ * (src/lighthouse_selection_cuda.py:370-397).
+ * strict = 1 reproduces the reference's domain (LH_ERR_DOMAIN outside it);
+ * strict = 0 admits any shape with per-tile compaction.
+ * Any output pointer may be NULL.
+ */
+int lh_select_geometry(int S, int L, int p, int topk, int strict,
+                       int *num_tiles, int *nodes_per_tile, int *per_tile, int *S_sel);
+
+/*
+ * Norm scorer + Q/K/V pyramid, one streaming pass.
+ * Replaces DialatedLighthouseNormScorer.forward (src/lighthouse_selection.py:589-616)
+ * and the pyramid half of DilatedLighthouseScorer.forward (:655-689).
+ *   xq, xk, xv      bf16 base rows, strides (sb, ss, sh) in elements, D contiguous
+ *   pq, pk, pv      bf16 pooled rows written for levels 2..L, strides (pb, ps, ph)
+ *   scores_qk/_kq   fp32 [B, H, S_tot] contiguous
+ *   base_scores_given = 0: base-level scores are the bf16-rounded L2 norms of
+ *     xq (qk) and xk (kq); = 1: base-level scores are already in scores_*
+ *     (written by lh_dilated_scores) and only the max-pooled levels are made.
+ */
+int lh_pyramid_fwd(const void *xq, const void *xk, const void *xv,
+                   int64_t sb, int64_t ss, int64_t sh,
+                   void *pq, void *pk, void *pv,
+                   int64_t pb, int64_t ps, int64_t ph,
+                   float *scores_qk, float *scores_kq,
+                   int B, int S, int H, int D, int L, int p,
+                   int base_scores_given, void *stream);
+
+/*
+ * Dilated scorer base scores: ||causal_attn(q,k,v)||_2 and ||causal_attn(k,q,v)||_2
+ * over the dilated virtual heads, written to scores_qk/_kq[:, :, 0:S].
+ * Replaces the two SDPA calls and norms of DilatedLighthouseScorer.forward
+ * (src/lighthouse_selection.py:638-653).  Inputs are contiguous [B, S, H, D].
+ */
+int lh_dilated_scores(const void *xq, const void *xk, const void *xv,
+                      float *scores_qk, float *scores_kq,
+                      int B, int S, int H, int D, int dilation, int S_tot, void *stream);
+
+/*
+ * Hierarchical per-tile top-k selection, emitted in causal order.
+ * Replaces lighthouse_selection_chunked_topk_kernel + torch.sort/gather
+ * (src/lighthouse_selection_cuda.py:114-331, :399-427).
+ *   scores_qk/_kq  fp32 [B, H, S_tot] contiguous
+ *   indices        int32 [B, H, S_sel] (S_sel from lh_select_geometry)
+ *   inverse        int32 [B, H, S_tot] or NULL
+ *   tie_mode       LH_TIE_REFERENCE or LH_TIE_LOWER_INDEX
+ */
+int lh_select_topk(const float *scores_qk, const float *scores_kq,
+                   int32_t *indices, int32_t *inverse,
+                   int B, int H, int S, int L, int p, int topk,
+                   int tie_mode, int strict, void *stream);
+
+/*
+ * inverse[b,h,r] = s where indices[b,h,s] == r, else -1.  (Device helper for
+ * callers holding only `indices`, e.g. scatter_to_base_sequence.)
+ */
+int lh_build_inverse(const int32_t *indices, int n, int32_t *inverse, int S_tot,
+                     int B, int H, void *stream);
+
+/*
+ * Causal attention over gathered rows, forward.
+ * Replaces the three torch.gather calls + self.attention(...)
+ * (src/lighthouse_selection.py:800-815).
+ * Row r of (b, h) is read from
+ *   base + b*sb + r*ss + h*sh            if r <  split
+ *   pool + b*pb + (r-split)*ps + h*ph    if r >= split
+ * where r = indices[b,h,s] (or r = s when indices == NULL).
+ *   out  bf16 [B, H, n, D];  lse fp32 [B, H, n] (log2-domain: m*log2(e)+log2(sum))
+ */
+int lh_attn_fwd(const void *q, const void *k, const void *v, int64_t sb, int64_t ss, int64_t sh,
+                const void *qp, const void *kp, const void *vp, int64_t pb, int64_t ps, int64_t ph,
+                int split, const int32_t *indices, int B, int H, int n, int D, float scale,
+                void *out, float *lse, void *stream);
+
+/*
+ * Causal attention backward over gathered rows (deterministic: dK/dV per key
+ * block, dQ per query block, no atomics).  Replaces the SDPA backward and the
+ * gather backward's row selection (src/lighthouse_selection.py:800-815).
+ *   dout   bf16 [B, H, n, D] (from lh_scatter_bwd); lse, delta fp32 [B, H, n]
+ *   dq, dk, dv bf16 [B, H, n, D] in selected order
+ */
+int lh_attn_bwd(const void *q, const void *k, const void *v, int64_t sb, int64_t ss, int64_t sh,
+                const void *qp, const void *kp, const void *vp, int64_t pb, int64_t ps, int64_t ph,
+                int split, const int32_t *indices, int B, int H, int n, int D, float scale,
+                const void *dout, const float *lse, const float *delta,
+                void *dq, void *dk, void *dv, void *stream);
+
+/*
+ * Fan-out of each selected row onto the base positions it stands for:
+ * out[b,h,t] = sum over levels l of attn[b,h,inverse[b,h,off_l + (t+1)/c_l - 1]].
+ * Replaces _scatter_fanout_fwd_kernel / _ScatterToBaseAutograd.forward
+ * (src/lighthouse_selection.py:408-459, :519-550) without atomics.
+ *   attn bf16 [B, H, n, D]; out bf16 [B, H, S_out, D] (rows >= S are zero)
+ */
+int lh_scatter_fwd(const void *attn, const int32_t *inverse, void *out,
+                   int B, int H, int S, int S_out, int n, int D, int L, int p, void *stream);
+
+/*
+ * Adjoint of the fan-out: dattn[s] = sum of dout over the span of entry s,
+ * plus delta[s] = sum_d bf16(dattn[s,d]) * o[s,d] for the attention backward
+ * (delta is skipped when o or delta is NULL).
+ * Replaces _scatter_fanout_bwd_kernel (src/lighthouse_selection.py:462-514, :552-576).
+ *   dout bf16 [B, H, S_out, D]
+ */
+int lh_scatter_bwd(const void *dout, const int32_t *indices, const void *o,
+                   void *dattn, float *delta,
+                   int B, int H, int S, int S_out, int n, int D, int L, int p, void *stream);
+
+/*
+ * Pyramid backward: dX[b,t,h] = g[inverse(t)] + sum_{l>=2} g[inverse(off_l + t/c_l)] / c_l
+ * for X in {q, k, v} at once (any of the three may be NULL).
+ * Replaces the autograd of torch.gather + torch.cat + mean
+ * (src/lighthouse_selection.py:604-614, :800-813).
+ *   gq, gk, gv  bf16 selected-space grads, strides (gb, gh, gs) in elements
+ *   inverse     int32 [B, H, S_tot]; NULL means the identity (g indexed by pyramid row)
+ *   dxq/dxk/dxv bf16 [B, S, H, D] contiguous
+ */
+int lh_pyramid_bwd(const void *gq, const void *gk, const void *gv,
+                   int64_t gb, int64_t gh, int64_t gs,
+                   const int32_t *inverse,
+                   void *dxq, void *dxk, void *dxv,
+                   int B, int S, int H, int D, int L, int p, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LIGHTHOUSE_HIP_H */

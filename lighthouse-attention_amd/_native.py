@@ -1,0 +1,310 @@
+"""ctypes binding of ``liblighthouse_hip.so`` (the gfx950 kernels behind the C ABI
+declared in ``include/lighthouse_hip.h``) and thin tensor-level wrappers.
+
+PyTorch is used only for device memory and the current HIP stream: every
+wrapper allocates its outputs with ``torch.empty`` and passes raw pointers,
+sizes and strides to the library, which launches on the caller's stream.
+There is no fallback: if the library is missing or a tensor is not on a GPU,
+the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liblighthouse_hip.so")
+CSRC = os.path.join(_HERE, "csrc")
+D_SUPPORTED = 128
+
+TIE_MODES = {"reference": 0, "lower_index": 1}
+
+_lib = None
+_lock = threading.Lock()
+
+_c = ctypes
+_P = _c.c_void_p
+_I = _c.c_int
+_L = _c.c_int64
+_F = _c.c_float
+
+_SIGS = {
+    "lh_strerror": (_c.c_char_p, [_I]),
+    "lh_abi_version": (_I, []),
+    "lh_select_geometry": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P]),
+    "lh_pyramid_fwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _P, _P,
+                            _I, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_dilated_scores": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_select_topk": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_build_inverse": (_I, [_P, _I, _P, _I, _I, _I, _P]),
+    "lh_attn_fwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _I, _P,
+                         _I, _I, _I, _I, _F, _P, _P, _P]),
+    "lh_attn_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _I, _P,
+                         _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P]),
+    "lh_scatter_fwd": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_scatter_bwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_pyramid_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+}
+EXPORTED = tuple(_SIGS)
+
+
+def build(force: bool = True, jobs: int = 5) -> str:
+    """Compile ``liblighthouse_hip.so`` for gfx950 with hipcc (``csrc/Makefile``)."""
+    if force:
+        subprocess.run(["make", "-s", "-C", CSRC, "clean"], check=True)
+    subprocess.run(["make", "-s", f"-j{jobs}", "-C", CSRC], check=True)
+    return LIB_PATH
+
+
+def lib():
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise RuntimeError(
+                        f"{LIB_PATH} is missing: build it with `make -C {CSRC}` "
+                        "(or __graft_entry__.build()); there is no non-native fallback")
+                h = ctypes.CDLL(LIB_PATH)
+                for name, (res, args) in _SIGS.items():
+                    f = getattr(h, name)
+                    f.restype = res
+                    f.argtypes = args
+                _lib = h
+    return _lib
+
+
+class LighthouseHipError(RuntimeError):
+    pass
+
+
+def _check(rc: int, what: str):
+    if rc != 0:
+        msg = lib().lh_strerror(rc).decode()
+        raise LighthouseHipError(f"{what}: {msg} (code {rc})")
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _need_gpu(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise LighthouseHipError("lighthouse_hip kernels need GPU tensors (no CPU path)")
+
+
+def geometry(S: int, L: int, p: int, topk: int, strict: bool = True):
+    """``(num_tiles, nodes_per_tile, per_tile, S_sel)``; raises like the reference outside
+    its domain when ``strict``."""
+    out = [ctypes.c_int() for _ in range(4)]
+    rc = lib().lh_select_geometry(S, L, p, topk, int(bool(strict)), *[ctypes.byref(o) for o in out])
+    if rc == 2:
+        raise AssertionError(
+            f"selection geometry S={S}, num_levels={L}, pooling_factor={p}, topk={topk} is outside the "
+            "reference kernel's domain (N_CHUNK_COARSEST must be >= 128 and a multiple of 64, tiles must "
+            "divide the coarsest level); pass strict=False for per-tile compaction")
+    _check(rc, "lh_select_geometry")
+    return tuple(o.value for o in out)
+
+
+def pyramid_lengths(S: int, L: int, p: int):
+    lens = [S // p ** l for l in range(L)]
+    offs = [sum(lens[:l]) for l in range(L)]
+    return lens, offs, sum(lens)
+
+
+# ---------------------------------------------------------------------------
+# op wrappers (tensor in, tensor out; all on the current stream)
+# ---------------------------------------------------------------------------
+def pyramid_fwd(xq, xk, xv, L: int, p: int, scores=None, pooled_out=None):
+    """Norm scores + pooled Q/K/V.  ``xq/xk/xv`` bf16 [B, S, H, D] with D contiguous.
+
+    Returns ``(pq, pk, pv, scores_qk, scores_kq)`` with pooled rows bf16
+    [B, Sp, H, D] and scores fp32 [B, H, S_tot].  If ``scores`` is given
+    (dilated scorer), its base level is kept and only pooled.
+    ``pooled_out`` may supply three pooled destinations (any strides, D contiguous).
+    """
+    _need_gpu(xq, xk, xv)
+    B, S, H, D = xq.shape
+    assert xk.shape == xq.shape and xv.shape == xq.shape
+    assert xq.dtype == torch.bfloat16 and xk.dtype == torch.bfloat16 and xv.dtype == torch.bfloat16
+    assert xq.stride() == xk.stride() == xv.stride(), "q/k/v must share strides"
+    lens, offs, S_tot = pyramid_lengths(S, L, p)
+    Sp = S_tot - S
+    dev = xq.device
+    if pooled_out is None:
+        pq, pk, pv = (torch.empty(B, Sp, H, D, dtype=torch.bfloat16, device=dev) for _ in range(3))
+    else:
+        pq, pk, pv = pooled_out
+    if scores is None:
+        sqk = torch.empty(B, H, S_tot, dtype=torch.float32, device=dev)
+        skq = torch.empty_like(sqk)
+        given = 0
+    else:
+        sqk, skq = scores
+        given = 1
+    sb, ss, sh, _ = xq.stride()
+    pb, ps, ph, _ = pq.stride()
+    with torch.cuda.device(dev):
+        rc = lib().lh_pyramid_fwd(_ptr(xq), _ptr(xk), _ptr(xv), sb, ss, sh, _ptr(pq), _ptr(pk), _ptr(pv),
+                                  pb, ps, ph, _ptr(sqk), _ptr(skq), B, S, H, D, L, p, given, _stream(dev))
+    _check(rc, "lh_pyramid_fwd")
+    return pq, pk, pv, sqk, skq
+
+
+def dilated_scores(xq, xk, xv, dilation: int, S_tot: int):
+    """Base-level dilated scores into fresh fp32 [B, H, S_tot] buffers (pooled levels unset)."""
+    _need_gpu(xq, xk, xv)
+    B, S, H, D = xq.shape
+    for t in (xq, xk, xv):
+        assert t.is_contiguous() and t.dtype == torch.bfloat16
+    dev = xq.device
+    sqk = torch.empty(B, H, S_tot, dtype=torch.float32, device=dev)
+    skq = torch.empty_like(sqk)
+    with torch.cuda.device(dev):
+        rc = lib().lh_dilated_scores(_ptr(xq), _ptr(xk), _ptr(xv), _ptr(sqk), _ptr(skq), B, S, H, D, dilation,
+                                     S_tot, _stream(dev))
+    _check(rc, "lh_dilated_scores")
+    return sqk, skq
+
+
+def select_topk(scores_qk, scores_kq, S: int, L: int, p: int, topk: int, tie: str = "reference",
+                strict: bool = True, with_inverse: bool = True):
+    """int32 indices [B, H, S_sel] (+ inverse map [B, H, S_tot] or None)."""
+    _need_gpu(scores_qk, scores_kq)
+    assert scores_qk.dtype == torch.float32 and scores_kq.dtype == torch.float32
+    assert scores_qk.shape == scores_kq.shape
+    if tie not in TIE_MODES:
+        raise ValueError(f"tie_break must be one of {sorted(TIE_MODES)}, got {tie!r}")
+    B, H, S_tot = scores_qk.shape
+    _, _, S_tot_expected = pyramid_lengths(S, L, p)
+    assert S_tot >= S_tot_expected, "scores are shorter than the pyramid"
+    sqk = scores_qk.contiguous()
+    skq = scores_kq.contiguous()
+    _, _, _, S_sel = geometry(S, L, p, topk, strict)
+    dev = sqk.device
+    idx = torch.empty(B, H, S_sel, dtype=torch.int32, device=dev)
+    inv = torch.empty(B, H, S_tot, dtype=torch.int32, device=dev) if with_inverse else None
+    if with_inverse and S_tot != S_tot_expected:
+        raise AssertionError("inverse map needs scores of exactly the pyramid length")
+    with torch.cuda.device(dev):
+        rc = lib().lh_select_topk(_ptr(sqk), _ptr(skq), _ptr(idx), _ptr(inv), B, H, S, L, p, topk,
+                                  TIE_MODES[tie], int(bool(strict)), _stream(dev))
+    _check(rc, "lh_select_topk")
+    return idx, inv
+
+
+def build_inverse(indices, S_tot: int):
+    _need_gpu(indices)
+    idx = indices.contiguous()
+    assert idx.dtype == torch.int32
+    B, H, n = idx.shape
+    inv = torch.empty(B, H, S_tot, dtype=torch.int32, device=idx.device)
+    with torch.cuda.device(idx.device):
+        rc = lib().lh_build_inverse(_ptr(idx), n, _ptr(inv), S_tot, B, H, _stream(idx.device))
+    _check(rc, "lh_build_inverse")
+    return inv
+
+
+class Rows:
+    """Where row r of (b, h) lives: ``base`` [.., r, .., D] for r < split,
+    else ``pool`` at r - split.  Strides are in elements, D contiguous."""
+
+    def __init__(self, q, k, v, base_strides, qp=None, kp=None, vp=None, pool_strides=(0, 0, 0), split=None):
+        self.q, self.k, self.v = q, k, v
+        self.qp, self.kp, self.vp = qp, kp, vp
+        self.bs = tuple(int(s) for s in base_strides)
+        self.ps = tuple(int(s) for s in pool_strides)
+        self.split = int(split) if split is not None else 2 ** 31 - 1
+
+    def args(self):
+        return (_ptr(self.q), _ptr(self.k), _ptr(self.v), *self.bs,
+                _ptr(self.qp), _ptr(self.kp), _ptr(self.vp), *self.ps, self.split)
+
+
+def attn_fwd(rows: Rows, indices, B: int, H: int, n: int, D: int = D_SUPPORTED, scale: float | None = None):
+    """Causal attention over the rows named by ``indices`` [B, H, n] (None = identity).
+
+    Returns ``(O bf16 [B, H, n, D], lse fp32 [B, H, n])`` (lse in the exp2 domain)."""
+    _need_gpu(rows.q, indices)
+    dev = rows.q.device
+    scale = D ** -0.5 if scale is None else scale
+    idx = indices.contiguous() if indices is not None else None
+    out = torch.empty(B, H, n, D, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, n, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib().lh_attn_fwd(*rows.args(), _ptr(idx), B, H, n, D, scale, _ptr(out), _ptr(lse), _stream(dev))
+    _check(rc, "lh_attn_fwd")
+    return out, lse
+
+
+def attn_bwd(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D: int = D_SUPPORTED,
+             scale: float | None = None):
+    """Gradients w.r.t. the gathered q, k, v rows: three bf16 [B, H, n, D]."""
+    _need_gpu(rows.q, dout)
+    dev = rows.q.device
+    scale = D ** -0.5 if scale is None else scale
+    idx = indices.contiguous() if indices is not None else None
+    dout = dout.contiguous()
+    dq, dk, dv = (torch.empty(B, H, n, D, dtype=torch.bfloat16, device=dev) for _ in range(3))
+    with torch.cuda.device(dev):
+        rc = lib().lh_attn_bwd(*rows.args(), _ptr(idx), B, H, n, D, scale, _ptr(dout), _ptr(lse), _ptr(delta),
+                               _ptr(dq), _ptr(dk), _ptr(dv), _stream(dev))
+    _check(rc, "lh_attn_bwd")
+    return dq, dk, dv
+
+
+def scatter_fwd(attn, inverse, S: int, S_out: int, L: int, p: int):
+    _need_gpu(attn, inverse)
+    attn = attn.contiguous()
+    B, H, n, D = attn.shape
+    out = torch.empty(B, H, S_out, D, dtype=attn.dtype, device=attn.device)
+    with torch.cuda.device(attn.device):
+        rc = lib().lh_scatter_fwd(_ptr(attn), _ptr(inverse), _ptr(out), B, H, S, S_out, n, D, L, p,
+                                  _stream(attn.device))
+    _check(rc, "lh_scatter_fwd")
+    return out
+
+
+def scatter_bwd(dout, indices, o, S: int, L: int, p: int):
+    """``(dattn bf16 [B, H, n, D], delta fp32 [B, H, n] or None)``."""
+    _need_gpu(dout, indices)
+    dout = dout.contiguous()
+    B, H, S_out, D = dout.shape
+    n = indices.shape[-1]
+    dattn = torch.empty(B, H, n, D, dtype=dout.dtype, device=dout.device)
+    delta = torch.empty(B, H, n, dtype=torch.float32, device=dout.device) if o is not None else None
+    oc = o.contiguous() if o is not None else None
+    with torch.cuda.device(dout.device):
+        rc = lib().lh_scatter_bwd(_ptr(dout), _ptr(indices.contiguous()), _ptr(oc), _ptr(dattn), _ptr(delta),
+                                  B, H, S, S_out, n, D, L, p, _stream(dout.device))
+    _check(rc, "lh_scatter_bwd")
+    return dattn, delta
+
+
+def pyramid_bwd(gq, gk, gv, inverse, B: int, S: int, H: int, L: int, p: int, D: int = D_SUPPORTED):
+    """Base-row gradients bf16 [B, S, H, D] from selected-space (or pyramid-row) grads
+    ``g*`` indexed [b, h, s, :] with any strides (D contiguous)."""
+    ref = next(g for g in (gq, gk, gv) if g is not None)
+    _need_gpu(ref)
+    dev = ref.device
+    outs = [torch.empty(B, S, H, D, dtype=torch.bfloat16, device=dev) if g is not None else None
+            for g in (gq, gk, gv)]
+    gb, gh, gs, _ = ref.stride()
+    for g in (gq, gk, gv):
+        assert g is None or tuple(g.stride()) == (gb, gh, gs, 1), "selected grads must share strides"
+    with torch.cuda.device(dev):
+        rc = lib().lh_pyramid_bwd(_ptr(gq), _ptr(gk), _ptr(gv), gb, gh, gs, _ptr(inverse),
+                                  _ptr(outs[0]), _ptr(outs[1]), _ptr(outs[2]), B, S, H, D, L, p, _stream(dev))
+    _check(rc, "lh_pyramid_bwd")
+    return tuple(outs)

@@ -1,0 +1,92 @@
+// Shared device/host helpers for the gfx950 Lighthouse kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/lighthouse_hip.h"
+
+#define LH_D 128  // head dimension supported by every kernel in this library
+
+typedef uint16_t bf16_t;  // bfloat16 storage
+typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef float floatx16 __attribute__((__vector_size__(16 * sizeof(float))));
+typedef float floatx4 __attribute__((__vector_size__(4 * sizeof(float))));
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(bf16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+
+// Round-to-nearest-even, NaN kept quiet.  Same rounding as torch's bf16 casts.
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (bf16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// 8 bf16 held in one 16-byte register quad.
+__device__ __forceinline__ void unpack8(const uint4 v, float* f) {
+  f[0] = __uint_as_float(v.x << 16); f[1] = __uint_as_float(v.x & 0xffff0000u);
+  f[2] = __uint_as_float(v.y << 16); f[3] = __uint_as_float(v.y & 0xffff0000u);
+  f[4] = __uint_as_float(v.z << 16); f[5] = __uint_as_float(v.z & 0xffff0000u);
+  f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xffff0000u);
+}
+
+__device__ __forceinline__ uint4 pack8(const float* f) {
+  uint4 v;
+  v.x = pack_bf16x2(f[0], f[1]); v.y = pack_bf16x2(f[2], f[3]);
+  v.z = pack_bf16x2(f[4], f[5]); v.w = pack_bf16x2(f[6], f[7]);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// pyramid geometry (integer forms)
+// ---------------------------------------------------------------------------
+// Level l (1-based) has S / p^(l-1) nodes; levels are concatenated base first.
+struct Pyramid {
+  int S, L, p;
+  int len[9];  // len[l] for l = 1..L
+  int off[9];  // off[l] for l = 1..L
+  int total;   // S_tot
+};
+
+static inline bool make_pyramid(int S, int L, int p, Pyramid* g) {
+  if (S <= 0 || L < 1 || L > 8 || p < 2) return false;
+  g->S = S; g->L = L; g->p = p;
+  long long c = 1, acc = 0;
+  for (int l = 1; l <= L; ++l) {
+    g->len[l] = (int)(S / c);
+    g->off[l] = (int)acc;
+    acc += g->len[l];
+    c *= p;
+    if (c > (1LL << 30)) return false;
+  }
+  g->total = (int)acc;
+  return true;
+}
+
+static inline int ipow(int b, int e) {
+  int r = 1;
+  for (int i = 0; i < e; ++i) r *= b;
+  return r;
+}
+
+static inline int ilog2_exact(int p) {
+  int s = 0;
+  while ((1 << s) < p) ++s;
+  return ((1 << s) == p) ? s : -1;
+}
+
+#define LH_CHECK_LAUNCH()                                  \
+  do {                                                     \
+    hipError_t _e = hipGetLastError();                     \
+    if (_e != hipSuccess) return LH_ERR_LAUNCH;            \
+  } while (0)

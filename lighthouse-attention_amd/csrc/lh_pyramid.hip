@@ -1,0 +1,237 @@
+// Norm scorer + mean-pooled Q/K/V pyramid (forward) and the pyramid backward.
+//
+// Forward restates DialatedLighthouseNormScorer.forward
+// (src/lighthouse_selection.py:589-616): base scores are the L2 norms of q and
+// k rows, rounded to bf16 like torch's bf16 `norm`; level j = 1..L-1 rows are
+// the means of p^j consecutive base rows (fp32 sum, one rounding), and level-j
+// scores are maxima of the base scores over the same span.  One pass streams
+// xq/xk/xv once: 16 lanes own one (b, span, head) unit, 8 bf16 each, and walk
+// the p^(L-1) base tokens of the span.  Base rows are never copied: pooled rows
+// go to a separate [B, Sp, H, D] buffer.
+//
+// Backward restates the autograd of gather + cat + mean: each base row gets
+// its own selected-space gradient plus, for every pooled level that contains
+// it, that node's gradient / c_l.  Gather-formulated through the inverse map,
+// so there are no atomics and the result is deterministic.
+#include "lh_common.h"
+
+namespace {
+
+struct PyrArgs {
+  const bf16_t *xq, *xk, *xv;
+  int64_t sb, ss, sh;
+  bf16_t *pq, *pk, *pv;
+  int64_t pb, ps, ph;
+  float *sqk, *skq;
+  int B, S, H, L, shift, S_tot, nspan, cmax, units;
+  int off[9];
+};
+
+__device__ __forceinline__ uint4 ld16(const bf16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+template <int NL, bool GIVEN>
+__global__ __launch_bounds__(256) void pyramid_fwd_kernel(const PyrArgs a) {
+  const int tid = threadIdx.x;
+  const int u = blockIdx.x * 16 + (tid >> 4);
+  const int l16 = tid & 15;
+  if (u >= a.units) return;
+  const int h = u % a.H;
+  const int rest = u / a.H;
+  const int span = rest % a.nspan;
+  const int b = rest / a.nspan;
+  const int t0 = span * a.cmax;
+  const int t1 = min(a.S, t0 + a.cmax);
+  const size_t srow = (size_t)(b * a.H + h) * a.S_tot;
+
+  constexpr int NA = NL > 0 ? NL : 1;
+  float accq[NA][8], acck[NA][8], accv[NA][8], mq[NA], mk[NA];
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+    mq[l] = -INFINITY; mk[l] = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { accq[l][e] = 0.f; acck[l][e] = 0.f; accv[l][e] = 0.f; }
+  }
+  const int64_t xoff = (int64_t)b * a.sb + (int64_t)h * a.sh + 8 * l16;
+  for (int t = t0; t < t1; ++t) {
+    const int64_t o = xoff + (int64_t)t * a.ss;
+    float fq[8], fk[8], fv[8];
+    unpack8(ld16(a.xq + o), fq);
+    unpack8(ld16(a.xk + o), fk);
+    unpack8(ld16(a.xv + o), fv);
+    float sq, sk;
+    if (GIVEN) {
+      sq = a.sqk[srow + t];
+      sk = a.skq[srow + t];
+    } else {
+      float pq = 0.f, pk = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { pq = fmaf(fq[e], fq[e], pq); pk = fmaf(fk[e], fk[e], pk); }
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) { pq += __shfl_xor(pq, m, 16); pk += __shfl_xor(pk, m, 16); }
+      sq = bf16_to_f32(f32_to_bf16(sqrtf(pq)));
+      sk = bf16_to_f32(f32_to_bf16(sqrtf(pk)));
+      if (l16 == 0) { a.sqk[srow + t] = sq; a.skq[srow + t] = sk; }
+    }
+#pragma unroll
+    for (int l = 0; l < NL; ++l) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { accq[l][e] += fq[e]; acck[l][e] += fk[e]; accv[l][e] += fv[e]; }
+      mq[l] = fmaxf(mq[l], sq);
+      mk[l] = fmaxf(mk[l], sk);
+      const int cs = (l + 1) * a.shift;  // log2 of the span of level l+2
+      if (((t + 1) & ((1 << cs) - 1)) == 0) {
+        const int node = t >> cs;
+        const int lvl = l + 2;
+        const float inv_c = 1.0f / (float)(1 << cs);
+        float mo[8];
+        const int64_t prow = (int64_t)b * a.pb + (int64_t)(a.off[lvl] - a.S + node) * a.ps + (int64_t)h * a.ph + 8 * l16;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mo[e] = accq[l][e] * inv_c;
+        *reinterpret_cast<uint4*>(a.pq + prow) = pack8(mo);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mo[e] = acck[l][e] * inv_c;
+        *reinterpret_cast<uint4*>(a.pk + prow) = pack8(mo);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mo[e] = accv[l][e] * inv_c;
+        *reinterpret_cast<uint4*>(a.pv + prow) = pack8(mo);
+        if (l16 == 0) {
+          a.sqk[srow + a.off[lvl] + node] = mq[l];
+          a.skq[srow + a.off[lvl] + node] = mk[l];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { accq[l][e] = 0.f; acck[l][e] = 0.f; accv[l][e] = 0.f; }
+        mq[l] = -INFINITY; mk[l] = -INFINITY;
+      }
+    }
+  }
+}
+
+struct PyrBwdArgs {
+  const bf16_t *gq, *gk, *gv;
+  int64_t gb, gh, gs;
+  const int32_t* inv;
+  bf16_t *dq, *dk, *dv;
+  int B, S, H, L, shift, S_tot;
+  int off[9], len[9];
+  long long rows;
+};
+
+__global__ __launch_bounds__(256) void pyramid_bwd_kernel(const PyrBwdArgs a) {
+  const int tid = threadIdx.x;
+  const long long row = (long long)blockIdx.x * 16 + (tid >> 4);
+  const int l16 = tid & 15;
+  if (row >= a.rows) return;
+  const int h = (int)(row % a.H);
+  const long long bt = row / a.H;
+  const int t = (int)(bt % a.S);
+  const int b = (int)(bt / a.S);
+  const size_t irow = (size_t)(b * a.H + h) * a.S_tot;
+  const int64_t gbase = (int64_t)b * a.gb + (int64_t)h * a.gh + 8 * l16;
+  float fq[8] = {0}, fk[8] = {0}, fv[8] = {0};
+  for (int lvl = 1; lvl <= a.L; ++lvl) {
+    const int cs = (lvl - 1) * a.shift;
+    const int node = t >> cs;
+    if (node >= a.len[lvl]) continue;
+    const int r = a.off[lvl] + node;
+    const int s = a.inv ? a.inv[irow + r] : r;
+    if (s < 0) continue;
+    const float w = 1.0f / (float)(1 << cs);
+    const int64_t go = gbase + (int64_t)s * a.gs;
+    float g[8];
+    if (a.gq) { unpack8(ld16(a.gq + go), g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) fq[e] = fmaf(g[e], w, fq[e]); }
+    if (a.gk) { unpack8(ld16(a.gk + go), g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) fk[e] = fmaf(g[e], w, fk[e]); }
+    if (a.gv) { unpack8(ld16(a.gv + go), g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) fv[e] = fmaf(g[e], w, fv[e]); }
+  }
+  const size_t o = (size_t)row * LH_D + 8 * l16;
+  if (a.dq) *reinterpret_cast<uint4*>(a.dq + o) = pack8(fq);
+  if (a.dk) *reinterpret_cast<uint4*>(a.dk + o) = pack8(fk);
+  if (a.dv) *reinterpret_cast<uint4*>(a.dv + o) = pack8(fv);
+}
+
+template <int NL>
+int launch_fwd(const PyrArgs& a, bool given, hipStream_t st) {
+  const int blocks = (a.units + 15) / 16;
+  if (given)
+    hipLaunchKernelGGL((pyramid_fwd_kernel<NL, true>), dim3(blocks), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((pyramid_fwd_kernel<NL, false>), dim3(blocks), dim3(256), 0, st, a);
+  LH_CHECK_LAUNCH();
+  return LH_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" int lh_pyramid_fwd(const void* xq, const void* xk, const void* xv, int64_t sb, int64_t ss, int64_t sh,
+                              void* pq, void* pk, void* pv, int64_t pb, int64_t ps, int64_t ph,
+                              float* scores_qk, float* scores_kq, int B, int S, int H, int D, int L, int p,
+                              int base_scores_given, void* stream) {
+  if (D != LH_D) return LH_ERR_UNSUPPORTED;
+  if (!xq || !xk || !xv || !scores_qk || !scores_kq || B <= 0 || H <= 0 || S <= 0) return LH_ERR_INVALID_ARG;
+  const int shift = ilog2_exact(p);
+  if (shift <= 0 || L < 1) return LH_ERR_INVALID_ARG;
+  if (L > 6) return LH_ERR_UNSUPPORTED;
+  if (L > 1 && (!pq || !pk || !pv)) return LH_ERR_INVALID_ARG;
+  if ((sb | ss | sh) % 8 || (L > 1 && (pb | ps | ph) % 8)) return LH_ERR_INVALID_ARG;
+  if (!aligned16(xq) || !aligned16(xk) || !aligned16(xv) || (L > 1 && (!aligned16(pq) || !aligned16(pk) || !aligned16(pv))))
+    return LH_ERR_INVALID_ARG;
+  Pyramid g;
+  if (!make_pyramid(S, L, p, &g)) return LH_ERR_INVALID_ARG;
+  PyrArgs a{};
+  a.xq = (const bf16_t*)xq; a.xk = (const bf16_t*)xk; a.xv = (const bf16_t*)xv;
+  a.sb = sb; a.ss = ss; a.sh = sh;
+  a.pq = (bf16_t*)pq; a.pk = (bf16_t*)pk; a.pv = (bf16_t*)pv;
+  a.pb = pb; a.ps = ps; a.ph = ph;
+  a.sqk = scores_qk; a.skq = scores_kq;
+  a.B = B; a.S = S; a.H = H; a.L = L; a.shift = shift; a.S_tot = g.total;
+  a.cmax = ipow(p, L - 1);
+  if (a.cmax > 4096) return LH_ERR_UNSUPPORTED;
+  a.nspan = (S + a.cmax - 1) / a.cmax;
+  const long long units = (long long)B * a.nspan * H;
+  if (units > (1LL << 30)) return LH_ERR_UNSUPPORTED;
+  a.units = (int)units;
+  for (int l = 1; l <= L; ++l) a.off[l] = g.off[l];
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool given = base_scores_given != 0;
+  switch (L - 1) {
+    case 0: return launch_fwd<0>(a, given, st);
+    case 1: return launch_fwd<1>(a, given, st);
+    case 2: return launch_fwd<2>(a, given, st);
+    case 3: return launch_fwd<3>(a, given, st);
+    case 4: return launch_fwd<4>(a, given, st);
+    default: return launch_fwd<5>(a, given, st);
+  }
+}
+
+extern "C" int lh_pyramid_bwd(const void* gq, const void* gk, const void* gv, int64_t gb, int64_t gh, int64_t gs,
+                              const int32_t* inverse, void* dxq, void* dxk, void* dxv, int B, int S, int H, int D,
+                              int L, int p, void* stream) {
+  if (D != LH_D) return LH_ERR_UNSUPPORTED;
+  if (B <= 0 || H <= 0 || S <= 0 || L < 1 || L > 8) return LH_ERR_INVALID_ARG;
+  const int shift = ilog2_exact(p);
+  if (shift <= 0) return LH_ERR_INVALID_ARG;
+  if ((gq != nullptr) != (dxq != nullptr) || (gk != nullptr) != (dxk != nullptr) || (gv != nullptr) != (dxv != nullptr))
+    return LH_ERR_INVALID_ARG;
+  if ((gb | gh | gs) % 8) return LH_ERR_INVALID_ARG;
+  Pyramid g;
+  if (!make_pyramid(S, L, p, &g)) return LH_ERR_INVALID_ARG;
+  PyrBwdArgs a{};
+  a.gq = (const bf16_t*)gq; a.gk = (const bf16_t*)gk; a.gv = (const bf16_t*)gv;
+  a.gb = gb; a.gh = gh; a.gs = gs; a.inv = inverse;
+  a.dq = (bf16_t*)dxq; a.dk = (bf16_t*)dxk; a.dv = (bf16_t*)dxv;
+  a.B = B; a.S = S; a.H = H; a.L = L; a.shift = shift; a.S_tot = g.total;
+  for (int l = 1; l <= L; ++l) { a.off[l] = g.off[l]; a.len[l] = g.len[l]; }
+  a.rows = (long long)B * S * H;
+  const long long blocks = (a.rows + 15) / 16;
+  if (blocks > 2147483647LL) return LH_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(pyramid_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+  LH_CHECK_LAUNCH();
+  return LH_OK;
+}

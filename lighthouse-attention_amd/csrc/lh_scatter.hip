@@ -1,0 +1,136 @@
+// Fan-out of selected rows onto the base sequence (forward) and its adjoint.
+//
+// Forward restates _scatter_fanout_fwd_kernel (src/lighthouse_selection.py:408-459):
+// the entry at level l, local index i, is added to base positions
+// [(i+1)c_l - 1, (i+2)c_l - 2].  Turned around, base position t receives, from
+// each level, the node floor((t+1)/c_l) - 1 if that node was selected.  Each
+// output row therefore gathers at most L rows through the inverse map, sums in
+// fp32 and rounds once: no zero-fill, no atomics, deterministic.
+//
+// Backward restates _scatter_fanout_bwd_kernel (:462-514): each selected row
+// sums dout over its span.  The same pass forms delta = rowsum(dattn * o) for
+// the attention backward from the bf16-rounded dattn, as SDPA's backward does.
+#include "lh_common.h"
+
+namespace {
+
+struct ScatArgs {
+  const bf16_t* src;       // fwd: attn [BH, n, D];  bwd: dout [BH, S_out, D]
+  const int32_t* map;      // fwd: inverse [BH, S_tot];  bwd: indices [BH, n]
+  const bf16_t* o;         // bwd: attention output [BH, n, D] (optional)
+  bf16_t* dst;             // fwd: out [BH, S_out, D];  bwd: dattn [BH, n, D]
+  float* delta;            // bwd: [BH, n] (optional)
+  int S, S_out, n, L, shift, S_tot;
+  int off[9], len[9];
+  long long rows;
+};
+
+__device__ __forceinline__ uint4 ld16(const bf16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+__global__ __launch_bounds__(256) void scatter_fwd_kernel(const ScatArgs a) {
+  const int tid = threadIdx.x;
+  const long long row = (long long)blockIdx.x * 16 + (tid >> 4);
+  const int l16 = tid & 15;
+  if (row >= a.rows) return;
+  const int t = (int)(row % a.S_out);
+  const long long bh = row / a.S_out;
+  const int32_t* inv = a.map + bh * a.S_tot;
+  const bf16_t* src = a.src + (size_t)bh * a.n * LH_D + 8 * l16;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int lvl = 1; lvl <= a.L; ++lvl) {
+    const int cs = (lvl - 1) * a.shift;
+    const int node = ((t + 1) >> cs) - 1;
+    if (node < 0 || node >= a.len[lvl]) continue;
+    const int s = inv[a.off[lvl] + node];
+    if (s < 0) continue;
+    float f[8];
+    unpack8(ld16(src + (size_t)s * LH_D), f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += f[e];
+  }
+  *reinterpret_cast<uint4*>(a.dst + (size_t)row * LH_D + 8 * l16) = pack8(acc);
+}
+
+__global__ __launch_bounds__(256) void scatter_bwd_kernel(const ScatArgs a) {
+  const int tid = threadIdx.x;
+  const long long row = (long long)blockIdx.x * 16 + (tid >> 4);
+  const int l16 = tid & 15;
+  if (row >= a.rows) return;  // all 16 lanes of a row leave together
+  const long long bh = row / a.n;
+  const int r = a.map[row];
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (r >= 0 && r < a.S_tot) {
+    int lvl = 1;
+    while (lvl < a.L && r >= a.off[lvl + 1]) ++lvl;
+    const int cs = (lvl - 1) * a.shift;
+    const int c = 1 << cs;
+    const int local = r - a.off[lvl];
+    const int start = local * c + c - 1;
+    const int stop = min(start + c, a.S_out);
+    const bf16_t* src = a.src + (size_t)bh * a.S_out * LH_D + 8 * l16;
+    for (int t = start; t < stop; ++t) {
+      float f[8];
+      unpack8(ld16(src + (size_t)t * LH_D), f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += f[e];
+    }
+  }
+  const uint4 packed = pack8(acc);
+  *reinterpret_cast<uint4*>(a.dst + (size_t)row * LH_D + 8 * l16) = packed;
+  if (a.delta) {
+    float g[8], o[8];
+    unpack8(packed, g);
+    unpack8(ld16(a.o + (size_t)row * LH_D + 8 * l16), o);
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d = fmaf(g[e], o[e], d);
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) d += __shfl_xor(d, m, 16);
+    if (l16 == 0) a.delta[row] = d;
+  }
+}
+
+int fill(ScatArgs& a, int S, int S_out, int n, int L, int p, int B, int H) {
+  const int shift = ilog2_exact(p);
+  if (shift <= 0 || L < 1 || L > 8 || S <= 0 || S_out <= 0 || n < 0 || B <= 0 || H <= 0) return LH_ERR_INVALID_ARG;
+  Pyramid g;
+  if (!make_pyramid(S, L, p, &g)) return LH_ERR_INVALID_ARG;
+  a.S = S; a.S_out = S_out; a.n = n; a.L = L; a.shift = shift; a.S_tot = g.total;
+  for (int l = 1; l <= L; ++l) { a.off[l] = g.off[l]; a.len[l] = g.len[l]; }
+  return LH_OK;
+}
+
+}  // namespace
+
+extern "C" int lh_scatter_fwd(const void* attn, const int32_t* inverse, void* out, int B, int H, int S, int S_out,
+                              int n, int D, int L, int p, void* stream) {
+  if (D != LH_D) return LH_ERR_UNSUPPORTED;
+  if (!attn || !inverse || !out) return LH_ERR_INVALID_ARG;
+  ScatArgs a{};
+  int rc = fill(a, S, S_out, n, L, p, B, H);
+  if (rc) return rc;
+  a.src = (const bf16_t*)attn; a.map = inverse; a.dst = (bf16_t*)out;
+  a.rows = (long long)B * H * S_out;
+  const long long blocks = (a.rows + 15) / 16;
+  if (blocks > 2147483647LL) return LH_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(scatter_fwd_kernel, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+  LH_CHECK_LAUNCH();
+  return LH_OK;
+}
+
+extern "C" int lh_scatter_bwd(const void* dout, const int32_t* indices, const void* o, void* dattn, float* delta,
+                              int B, int H, int S, int S_out, int n, int D, int L, int p, void* stream) {
+  if (D != LH_D) return LH_ERR_UNSUPPORTED;
+  if (!dout || !indices || !dattn || ((o == nullptr) != (delta == nullptr))) return LH_ERR_INVALID_ARG;
+  ScatArgs a{};
+  int rc = fill(a, S, S_out, n, L, p, B, H);
+  if (rc) return rc;
+  a.src = (const bf16_t*)dout; a.map = indices; a.o = (const bf16_t*)o; a.dst = (bf16_t*)dattn; a.delta = delta;
+  a.rows = (long long)B * H * n;
+  if (a.rows == 0) return LH_OK;
+  const long long blocks = (a.rows + 15) / 16;
+  if (blocks > 2147483647LL) return LH_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(scatter_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+  LH_CHECK_LAUNCH();
+  return LH_OK;
+}

@@ -1,0 +1,350 @@
+// Hierarchical per-tile top-k selection for gfx950.
+//
+// One 64-lane wave per (b, h, tile).  The 128-element working set of the
+// reference block (src/lighthouse_selection_cuda.py:150-157) lives in
+// registers: element e = 64*slot + lane.  Compare-exchanges at distance 64 are
+// in-lane; distances 1..32 are cross-lane shuffles.  The network, the batch
+// structure and the candidate order follow src/lighthouse_selection_cuda.py:
+//   - sort network:                 :41-110 (strict compare-exchange)
+//   - candidates (coarsest/children): :177-229
+//   - qk then kq streaming sorts:     :232-258
+//   - selected = [TQ | TK], parents:  :274-289, :324-327
+//
+// Output order.  The reference emits every valid candidate once (as a kq
+// reject, as one of the final [TQ | TK], or as a level-1 leaf) with an
+// order key, then sorts the keys (:11-25, :425-427).  Here the emitted set is
+// taken structurally (every candidate of every level, flagged selected or
+// not), each entry's integer key (key * 2^(L-1)) is set in an LDS bitmap over
+// the tile's key span, and an entry's output position is its rank among the
+// set bits.  Tiles own disjoint key ranges, so the result is tile-major and no
+// global sort is needed.  The same pass writes the inverse map
+// (pyramid index -> selected position, -1 elsewhere) for the tile's pyramid
+// ranges; the last tile also clears the trailing nodes no tile visits.
+#include "lh_common.h"
+
+namespace {
+
+constexpr int TOPK = 128;
+constexpr int HALF = 64;
+constexpr float SENT = -1e6f;
+
+struct SelParams {
+  int S, L, p, shift, T, NCC, per_tile, S_sel, S_tot;
+  int nc_pad;             // candidate slots per level, padded to 64
+  int off[9], len[9];     // pyramid level offsets and lengths
+  int R[9];               // nodes of level l inside one tile
+  int selw_off[9];        // word offset of level l's selected bitmask (l >= 2)
+  int sel_words;          // total selected-bitmask words
+  int key_words;          // words of the key bitmap
+  int lds_bytes;
+};
+
+// ---------------------------------------------------------------------------
+// compare-exchange at lane distance j (1..32) for one slot
+// ---------------------------------------------------------------------------
+template <int TIE>
+__device__ __forceinline__ void cx_lane(float& s, int& x, int& id, int j, bool desc, int lane) {
+  const float os = __shfl_xor(s, j);
+  const int ox = __shfl_xor(x, j);
+  const int oid = TIE ? __shfl_xor(id, j) : 0;
+  const bool keep_max = (((lane & j) == 0) == desc);
+  bool take;
+  if (TIE == LH_TIE_REFERENCE) {
+    take = keep_max ? (s < os) : (s > os);
+  } else {
+    const unsigned mk = (unsigned)id, ok = (unsigned)oid;  // -1 -> largest: invalid ids lose ties
+    const bool other_better = (os > s) || (os == s && ok < mk);
+    const bool mine_better = (s > os) || (s == os && mk < ok);
+    take = keep_max ? other_better : mine_better;
+  }
+  if (take) { s = os; x = ox; id = oid; }
+}
+
+// Descending 128-wide bitonic sort; element e = 64*slot + lane.
+template <int TIE>
+__device__ __forceinline__ void sort128(float& s0, int& x0, int& i0, float& s1, int& x1, int& i1, int lane) {
+#pragma unroll
+  for (int k = 2; k <= TOPK; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j == 64) {  // k == 128: pair (lane, 64 + lane), descending
+        bool take;
+        if (TIE == LH_TIE_REFERENCE) {
+          take = s0 < s1;
+        } else {
+          take = (s1 > s0) || (s1 == s0 && (unsigned)i1 < (unsigned)i0);
+        }
+        if (take) {
+          float ts = s0; s0 = s1; s1 = ts;
+          int tx = x0; x0 = x1; x1 = tx;
+          int ti = i0; i0 = i1; i1 = ti;
+        }
+      } else {
+        const bool desc0 = (k >= 64) ? true : ((lane & k) == 0);
+        const bool desc1 = (k == 128) ? true : (k == 64 ? false : ((lane & k) == 0));
+        cx_lane<TIE>(s0, x0, i0, j, desc0, lane);
+        cx_lane<TIE>(s1, x1, i1, j, desc1, lane);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ bool get_bit(const uint32_t* bits, int i) {
+  return (bits[i >> 5] >> (i & 31)) & 1u;
+}
+
+template <int TIE>
+__global__ __launch_bounds__(64) void select_kernel(const float* __restrict__ sqk,
+                                                    const float* __restrict__ skq,
+                                                    int32_t* __restrict__ indices,
+                                                    int32_t* __restrict__ inverse,
+                                                    const SelParams P) {
+  const int tile = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int lane = threadIdx.x;
+  extern __shared__ uint32_t smem[];
+  float* sc_qk = reinterpret_cast<float*>(smem);
+  float* sc_kq = sc_qk + P.nc_pad;
+  int* cand = reinterpret_cast<int*>(sc_kq + P.nc_pad);
+  int* parent = cand + P.nc_pad;
+  uint32_t* selbits = reinterpret_cast<uint32_t*>(parent + TOPK);
+  uint32_t* kbits = selbits + P.sel_words;
+  uint32_t* kpre = kbits + P.key_words;
+
+  const float* q = sqk + (size_t)bh * P.S_tot;
+  const float* k = skq + (size_t)bh * P.S_tot;
+  const int L = P.L, p = P.p, shift = P.shift;
+
+  for (int w = lane; w < P.sel_words; w += 64) selbits[w] = 0u;
+  for (int w = lane; w < P.key_words; w += 64) kbits[w] = 0u;
+  parent[lane] = -1;
+  parent[lane + 64] = -1;
+  __syncthreads();
+
+  // ------------------------------------------------------------------ select
+  for (int level = L; level >= 2; --level) {
+    const int off = P.off[level];
+    const int nc = (level == L) ? P.NCC : p * TOPK;
+    const int nb = (nc + HALF - 1) / HALF;
+    for (int a = lane; a < nb * HALF; a += 64) {
+      int id = -1;
+      if (a < nc) {
+        if (level == L) {
+          id = tile * P.NCC + a;
+        } else {
+          const int par = parent[a >> shift];
+          if (par >= 0) id = par * p + (a & (p - 1));
+        }
+        if (id >= P.len[level]) id = -1;
+      }
+      cand[a] = id;
+      sc_qk[a] = id >= 0 ? q[off + id] : SENT;
+      sc_kq[a] = id >= 0 ? k[off + id] : SENT;
+    }
+    __syncthreads();
+
+    float tq_s = SENT, tk_s = SENT;
+    int tq_x = -1, tk_x = -1, tq_i = -1, tk_i = -1;
+    for (int b = 0; b < nb; ++b) {
+      const int a = b * HALF + lane;
+      float s0 = tq_s, s1 = sc_qk[a];
+      int x0 = tq_x, x1 = cand[a] >= 0 ? a : -1;
+      int i0 = tq_i, i1 = TIE ? cand[a] : 0;
+      sort128<TIE>(s0, x0, i0, s1, x1, i1, lane);
+      tq_s = s0; tq_x = x0; tq_i = i0;
+      // qk rejects (positions 64..127) stream into the kq sort
+      const int r = x1;
+      float u0 = tk_s, u1 = r >= 0 ? sc_kq[r] : SENT;
+      int y0 = tk_x, y1 = r;
+      int j0 = tk_i, j1 = TIE ? i1 : 0;
+      sort128<TIE>(u0, y0, j0, u1, y1, j1, lane);
+      tk_s = u0; tk_x = y0; tk_i = j0;
+    }
+    const int idq = tq_x >= 0 ? cand[tq_x] : -1;
+    const int idk = tk_x >= 0 ? cand[tk_x] : -1;
+    __syncthreads();  // every lane has read parent[] and cand[] for this level
+    parent[lane] = idq;
+    parent[lane + 64] = idk;
+    uint32_t* sb = selbits + P.selw_off[level];
+    const int base = tile * P.R[level];
+    if (idq >= 0) { const int t = idq - base; atomicOr(&sb[t >> 5], 1u << (t & 31)); }
+    if (idk >= 0) { const int t = idk - base; atomicOr(&sb[t >> 5], 1u << (t & 31)); }
+    __syncthreads();
+  }
+
+  // ------------------------------------------------------------------ rank
+  const int kscale_shift = L - 1;
+  const long long key_base = (long long)tile * P.NCC * ((long long)1 << ((L - 1) * shift)) << kscale_shift;
+  for (int level = L; level >= 1; --level) {
+    const int Rl = P.R[level];
+    const int base = tile * Rl;
+    const int c_shift = (level - 1) * shift;  // log2 c_l
+    for (int j = lane; j < Rl; j += 64) {
+      const bool is_cand = (level == L) || get_bit(selbits + P.selw_off[level + 1], j >> shift);
+      if (!is_cand) continue;
+      const bool is_sel = (level >= 2) && get_bit(selbits + P.selw_off[level], j);
+      const long long i = base + j;
+      const long long key = is_sel ? ((((i + 1) << c_shift) << kscale_shift) - (1LL << (L - level)))
+                                   : ((i << c_shift) << kscale_shift);
+      const int rel = (int)(key - key_base);
+      atomicOr(&kbits[rel >> 5], 1u << (rel & 31));
+    }
+  }
+  __syncthreads();
+  {  // exclusive prefix of popcounts per key word
+    const int chunk = (P.key_words + 63) / 64;
+    const int w0 = lane * chunk;
+    const int w1 = min(w0 + chunk, P.key_words);
+    int local = 0;
+    for (int w = w0; w < w1; ++w) local += __popc(kbits[w]);
+    int incl = local;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(incl, d);
+      if (lane >= d) incl += o;
+    }
+    int run = incl - local;
+    for (int w = w0; w < w1; ++w) { kpre[w] = (uint32_t)run; run += __popc(kbits[w]); }
+  }
+  __syncthreads();
+
+  // ------------------------------------------------------------------ emit
+  int32_t* out = indices + (size_t)bh * P.S_sel + (size_t)tile * P.per_tile;
+  int32_t* inv = inverse ? inverse + (size_t)bh * P.S_tot : nullptr;
+  for (int level = L; level >= 1; --level) {
+    const int Rl = P.R[level];
+    const int base = tile * Rl;
+    const int c_shift = (level - 1) * shift;
+    // the last tile also owns the trailing nodes that no tile visits
+    const int jend = (inv && tile == P.T - 1) ? (P.len[level] - base) : Rl;
+    for (int j = lane; j < jend; j += 64) {
+      int pos = -1;
+      if (j < Rl) {
+        const bool is_cand = (level == L) || get_bit(selbits + P.selw_off[level + 1], j >> shift);
+        if (is_cand) {
+          const bool is_sel = (level >= 2) && get_bit(selbits + P.selw_off[level], j);
+          const long long i = base + j;
+          const long long key = is_sel ? ((((i + 1) << c_shift) << kscale_shift) - (1LL << (L - level)))
+                                       : ((i << c_shift) << kscale_shift);
+          const int rel = (int)(key - key_base);
+          const int rank = (int)kpre[rel >> 5] + __popc(kbits[rel >> 5] & ((1u << (rel & 31)) - 1u));
+          if (rank < P.per_tile) {
+            out[rank] = P.off[level] + base + j;
+            pos = tile * P.per_tile + rank;
+          }
+        }
+      }
+      if (inv) inv[P.off[level] + base + j] = pos;
+    }
+  }
+}
+
+__global__ void fill_i32_kernel(int32_t* __restrict__ p, size_t n, int32_t v) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
+}
+
+__global__ void inverse_scatter_kernel(const int32_t* __restrict__ idx, int n, int32_t* __restrict__ inv,
+                                       int S_tot, int BH) {
+  const size_t total = (size_t)BH * n;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const int bh = (int)(i / n), s = (int)(i % n);
+    const int r = idx[i];
+    if (r >= 0 && r < S_tot) inv[(size_t)bh * S_tot + r] = s;
+  }
+}
+
+// Geometry shared by the host entry points.
+int geometry(int S, int L, int p, int topk, int strict, int* T, int* NCC, int* per_tile, int* S_sel,
+             Pyramid* pyr) {
+  if (L < 2 || L > 8 || p < 2 || (p & (p - 1)) || topk < TOPK || topk % TOPK || topk / 2 < p || S <= 0)
+    return LH_ERR_INVALID_ARG;
+  if (!make_pyramid(S, L, p, pyr)) return LH_ERR_INVALID_ARG;
+  const int t = topk / TOPK;
+  const int coarsest = pyr->len[L];
+  const int ncc = coarsest / t;
+  if (ncc < 1) return strict ? LH_ERR_DOMAIN : LH_ERR_INVALID_ARG;
+  if (strict) {
+    const int cL = ipow(p, L - 1);
+    if (ncc < TOPK || ncc % HALF || coarsest % t || S % cL) return LH_ERR_DOMAIN;
+  }
+  int n = ncc, total = ncc;
+  for (int l = L - 1; l >= 1; --l) {
+    n = p * (n < TOPK ? n : TOPK);
+    total += n;
+  }
+  *T = t; *NCC = ncc; *per_tile = total;
+  *S_sel = t * total;
+  return LH_OK;
+}
+
+}  // namespace
+
+extern "C" int lh_select_geometry(int S, int L, int p, int topk, int strict,
+                                  int* num_tiles, int* nodes_per_tile, int* per_tile, int* S_sel) {
+  int T, NCC, pt, ss;
+  Pyramid g;
+  const int rc = geometry(S, L, p, topk, strict, &T, &NCC, &pt, &ss, &g);
+  if (rc) return rc;
+  if (num_tiles) *num_tiles = T;
+  if (nodes_per_tile) *nodes_per_tile = NCC;
+  if (per_tile) *per_tile = pt;
+  if (S_sel) *S_sel = ss;
+  return LH_OK;
+}
+
+extern "C" int lh_select_topk(const float* scores_qk, const float* scores_kq, int32_t* indices,
+                              int32_t* inverse, int B, int H, int S, int L, int p, int topk,
+                              int tie_mode, int strict, void* stream) {
+  if (!scores_qk || !scores_kq || !indices || B <= 0 || H <= 0) return LH_ERR_INVALID_ARG;
+  if (tie_mode != LH_TIE_REFERENCE && tie_mode != LH_TIE_LOWER_INDEX) return LH_ERR_INVALID_ARG;
+  SelParams P{};
+  Pyramid g;
+  int rc = geometry(S, L, p, topk, strict, &P.T, &P.NCC, &P.per_tile, &P.S_sel, &g);
+  if (rc) return rc;
+  if ((long long)B * H > 65535 || P.T > 2147483647) return LH_ERR_UNSUPPORTED;
+  P.S = S; P.L = L; P.p = p; P.shift = ilog2_exact(p); P.S_tot = g.total;
+  for (int l = 1; l <= L; ++l) { P.off[l] = g.off[l]; P.len[l] = g.len[l]; }
+  const int ncmax = P.NCC > p * TOPK ? P.NCC : p * TOPK;
+  P.nc_pad = (ncmax + HALF - 1) / HALF * HALF;
+  int words = 0;
+  for (int l = L; l >= 1; --l) {
+    P.R[l] = P.NCC * ipow(p, L - l);
+    P.selw_off[l] = words;
+    if (l >= 2) words += (P.R[l] + 31) / 32;
+  }
+  P.sel_words = words;
+  // key span of one tile: NCC * c_L * 2^(L-1) integer keys
+  const long long span = (long long)P.NCC * ipow(p, L - 1) * (1LL << (L - 1));
+  if ((long long)S * ipow(p, 0) * (1LL << (L - 1)) >= (1LL << 31)) return LH_ERR_UNSUPPORTED;
+  P.key_words = (int)((span + 31) / 32);
+  const long long lds = 4LL * (3LL * P.nc_pad + TOPK + P.sel_words + 2LL * P.key_words);
+  if (lds > 65536) return LH_ERR_UNSUPPORTED;
+  P.lds_bytes = (int)lds;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid(P.T, B * H);
+  if (tie_mode == LH_TIE_REFERENCE)
+    hipLaunchKernelGGL(select_kernel<LH_TIE_REFERENCE>, grid, dim3(64), P.lds_bytes, st, scores_qk, scores_kq,
+                       indices, inverse, P);
+  else
+    hipLaunchKernelGGL(select_kernel<LH_TIE_LOWER_INDEX>, grid, dim3(64), P.lds_bytes, st, scores_qk, scores_kq,
+                       indices, inverse, P);
+  LH_CHECK_LAUNCH();
+  return LH_OK;
+}
+
+extern "C" int lh_build_inverse(const int32_t* indices, int n, int32_t* inverse, int S_tot, int B, int H,
+                                void* stream) {
+  if (!indices || !inverse || n < 0 || S_tot <= 0 || B <= 0 || H <= 0) return LH_ERR_INVALID_ARG;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const size_t tot = (size_t)B * H * S_tot;
+  const int blocks = (int)((tot + 255) / 256 < 65536 ? (tot + 255) / 256 : 65536);
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(blocks), dim3(256), 0, st, inverse, tot, -1);
+  LH_CHECK_LAUNCH();
+  if (n > 0) {
+    const size_t tn = (size_t)B * H * n;
+    const int b2 = (int)((tn + 255) / 256 < 65536 ? (tn + 255) / 256 : 65536);
+    hipLaunchKernelGGL(inverse_scatter_kernel, dim3(b2), dim3(256), 0, st, indices, n, inverse, S_tot, B * H);
+    LH_CHECK_LAUNCH();
+  }
+  return LH_OK;
+}

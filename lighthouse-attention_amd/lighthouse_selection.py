@@ -1,0 +1,407 @@
+"""Lighthouse selection attention on MI355X (gfx950): the ``lighthouse_selection``
+module API, backed by hand-written HIP kernels behind a C ABI.
+
+Drop-in for the reference module ``torchtitan/models/llama3/model/lighthouse_selection.py``
+(reference repository ``src/lighthouse_selection.py``): the names imported by the
+reference's model wiring (``lighthouse-attention.patch:591-598``) all exist here
+with the same constructor arguments and the same forward signatures.
+
+==================================  =====================================================
+name here                           reference
+==================================  =====================================================
+``DialatedLighthouseNormScorer``    ``src/lighthouse_selection.py:578-616``
+``DilatedLighthouseScorer``         ``src/lighthouse_selection.py:618-689``
+``DilatedLighthouseGLAScorer``      ``src/lighthouse_selection.py:692-755`` (not built)
+``LighthouseLocal``                 ``src/lighthouse_selection.py:772-825``
+``scatter_to_base_sequence``        ``src/lighthouse_selection.py:758-770``
+``DialatedLighthouseNormScorerCP``  ``src/lighthouse_selection.py:943-982`` (not built)
+``LighthouseCP``                    ``src/lighthouse_selection.py:985-1054`` (not built)
+``LighthouseSelectionQkKqChunkedTopkNvrtc``  ``src/lighthouse_selection_cuda.py:359-428``
+``compute_output_indices_selection``         ``src/lighthouse_selection_cuda.py:346-357``
+==================================  =====================================================
+
+Differences from the reference, all deliberate:
+  * ``LighthouseLocal`` runs the whole layer natively (pyramid, selection,
+    gathered causal attention with softmax scale 1/sqrt(D), fan-out) when its
+    scorer is one of this module's; the ``attention`` argument is kept for the
+    constructor signature and is only called when ``use_native_attention=False``.
+  * Selection is reference-exact by default (``tie_break="reference"``);
+    ``tie_break="lower_index"`` breaks score ties by lower index instead.
+  * ``strict=True`` (default) raises where the reference asserts or overruns
+    its output slots; ``strict=False`` compacts each tile's entries instead.
+  * ``DilatedLighthouseScorer``'s ``attention`` is optional and ``head_dim`` is
+    accepted, so the reference's own builder call (``lighthouse-attention.patch:623-628``)
+    constructs it.
+"""
+from __future__ import annotations
+
+import math
+from functools import lru_cache
+
+import torch
+import torch.nn as nn
+
+from . import _native as N
+
+__all__ = [
+    "DilatedLighthouseScorer", "DialatedLighthouseNormScorer", "DilatedLighthouseGLAScorer",
+    "LighthouseLocal", "DialatedLighthouseNormScorerCP", "LighthouseCP", "scatter_to_base_sequence",
+    "LighthouseSelectionQkKqChunkedTopkNvrtc", "LighthouseSelectionQkKqChunkedTopkHip",
+    "compute_output_indices_selection", "lighthouse_layer",
+]
+
+
+@lru_cache(maxsize=100)
+def compute_output_indices_selection(N_: int, num_levels: int, pooling_factor: int, topk: int) -> int:
+    """Selected length by the reference's formula (``src/lighthouse_selection_cuda.py:346-357``):
+    the coarsest level whole plus ``pooling_factor * topk`` per finer level."""
+    total = 0
+    for level in range(num_levels, 0, -1):
+        c_l = pooling_factor ** (level - 1)
+        total += N_ // c_l if level == num_levels else pooling_factor * topk
+    return total
+
+
+class LighthouseSelectionQkKqChunkedTopkHip:
+    """Per-tile hierarchical top-k selection (``src/lighthouse_selection_cuda.py:359-428``)."""
+
+    @staticmethod
+    @torch.no_grad()
+    def forward(scores_qk, scores_kq, num_levels, pooling_factor, topk, actual_seq_len,
+                tie_break: str = "reference", strict: bool = True):
+        assert scores_qk.shape == scores_kq.shape
+        assert scores_qk.is_cuda and scores_kq.is_cuda
+        assert scores_qk.dtype == torch.float32
+        assert topk % 128 == 0, "topk must be a multiple of 128"
+        assert (pooling_factor & (pooling_factor - 1)) == 0, "pf must be power of 2"
+        assert topk // 2 >= pooling_factor
+        idx, _ = N.select_topk(scores_qk.float(), scores_kq.float(), actual_seq_len, num_levels,
+                               pooling_factor, topk, tie=tie_break, strict=strict, with_inverse=False)
+        return idx
+
+
+# The reference's class name, so callers written against it keep working.
+LighthouseSelectionQkKqChunkedTopkNvrtc = LighthouseSelectionQkKqChunkedTopkHip
+
+
+# ---------------------------------------------------------------------------
+# autograd functions
+# ---------------------------------------------------------------------------
+def _base_rows(xq, xk, xv, pq=None, pk=None, pv=None):
+    S = xq.shape[1]
+    sb, ss, sh, _ = xq.stride()
+    if pq is None:
+        return N.Rows(xq, xk, xv, (sb, ss, sh))
+    pb, ps, ph, _ = pq.stride()
+    return N.Rows(xq, xk, xv, (sb, ss, sh), pq, pk, pv, (pb, ps, ph), split=S)
+
+
+class _LighthouseLayerFn(torch.autograd.Function):
+    """Whole layer: pyramid -> selection -> gathered causal attention -> fan-out.
+
+    Backward: fan-out adjoint (+ softmax delta) -> attention backward in
+    selected space -> pyramid backward onto the base rows.
+    """
+
+    @staticmethod
+    def forward(ctx, xq, xk, xv, L, p, topk, tie, strict, dilation):
+        B, S, H, D = xq.shape
+        xq, xk, xv = xq.contiguous(), xk.contiguous(), xv.contiguous()
+        lens, offs, S_tot = N.pyramid_lengths(S, L, p)
+        _, _, _, S_sel = N.geometry(S, L, p, topk, strict)
+        if dilation:
+            scores = N.dilated_scores(xq, xk, xv, dilation, S_tot)
+            pq, pk, pv, sqk, skq = N.pyramid_fwd(xq, xk, xv, L, p, scores=scores)
+        else:
+            pq, pk, pv, sqk, skq = N.pyramid_fwd(xq, xk, xv, L, p)
+        idx, inv = N.select_topk(sqk, skq, S, L, p, topk, tie=tie, strict=strict)
+        rows = _base_rows(xq, xk, xv, pq, pk, pv)
+        o, lse = N.attn_fwd(rows, idx, B, H, S_sel, D)
+        out = N.scatter_fwd(o, inv, S, S, L, p)
+        ctx.save_for_backward(xq, xk, xv, pq, pk, pv, idx, inv, o, lse)
+        ctx.geo = (B, S, H, D, L, p, S_sel)
+        ctx.mark_non_differentiable(idx)
+        return out, idx
+
+    @staticmethod
+    def backward(ctx, dout, _didx):
+        xq, xk, xv, pq, pk, pv, idx, inv, o, lse = ctx.saved_tensors
+        B, S, H, D, L, p, S_sel = ctx.geo
+        dattn, delta = N.scatter_bwd(dout, idx, o, S, L, p)
+        rows = _base_rows(xq, xk, xv, pq, pk, pv)
+        dqs, dks, dvs = N.attn_bwd(rows, idx, B, H, S_sel, dattn, lse, delta, D)
+        dxq, dxk, dxv = N.pyramid_bwd(dqs, dks, dvs, inv, B, S, H, L, p, D)
+        return dxq, dxk, dxv, None, None, None, None, None, None
+
+
+def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, topk: int = 1024,
+                     tie_break: str = "reference", strict: bool = True, dilation: int = 0):
+    """Functional form of the native layer: ``(out [B, H, S, D], indices [B, H, S_sel])``.
+
+    ``dilation > 0`` selects the dilated scorer, 0 the norm scorer."""
+    if xq.shape[-1] != N.D_SUPPORTED:
+        raise ValueError(f"head_dim must be {N.D_SUPPORTED}, got {xq.shape[-1]}")
+    if not (xq.shape == xk.shape == xv.shape):
+        raise AssertionError("xq, xk and xv must have the same shape (n_kv_heads == n_heads)")
+    for t in (xq, xk, xv):
+        if t.dtype != torch.bfloat16:
+            raise TypeError("the native layer computes in bfloat16; got " + str(t.dtype))
+    return _LighthouseLayerFn.apply(xq, xk, xv, num_levels, pooling_factor, topk, tie_break, strict,
+                                    int(dilation))
+
+
+class _PyramidCatFn(torch.autograd.Function):
+    """The reference scorer's 5-tuple from the native pyramid; backward through the
+    dense pyramid adjoint (``g[pyramid row]`` gathered onto base rows)."""
+
+    @staticmethod
+    def forward(ctx, xq, xk, xv, L, p, dilation, base_qk=None, base_kq=None):
+        B, S, H, D = xq.shape
+        xq, xk, xv = xq.contiguous(), xk.contiguous(), xv.contiguous()
+        _, _, S_tot = N.pyramid_lengths(S, L, p)
+        cats = [torch.empty(B, S_tot, H, D, dtype=xq.dtype, device=xq.device) for _ in range(3)]
+        for c, x in zip(cats, (xq, xk, xv)):
+            c[:, :S].copy_(x)
+        if base_qk is not None:  # base-level scores computed by the caller ([B, H, S])
+            scores = tuple(torch.empty(B, H, S_tot, dtype=torch.float32, device=xq.device) for _ in range(2))
+            scores[0][..., :S].copy_(base_qk)
+            scores[1][..., :S].copy_(base_kq)
+        else:
+            scores = N.dilated_scores(xq, xk, xv, dilation, S_tot) if dilation else None
+        _, _, _, sqk, skq = N.pyramid_fwd(xq, xk, xv, L, p, scores=scores,
+                                          pooled_out=tuple(c[:, S:] for c in cats))
+        ctx.geo = (B, S, H, D, L, p)
+        ctx.mark_non_differentiable(sqk, skq)
+        return (sqk.to(xq.dtype), skq.to(xq.dtype), cats[0].transpose(1, 2), cats[1].transpose(1, 2),
+                cats[2].transpose(1, 2))
+
+    @staticmethod
+    def backward(ctx, _g1, _g2, gq, gk, gv):
+        B, S, H, D, L, p = ctx.geo
+        gs = [g if g is not None else None for g in (gq, gk, gv)]
+        ref = next((g for g in gs if g is not None), None)
+        if ref is None:
+            return None, None, None, None, None, None, None, None
+        gs = [g.contiguous() if g is not None else torch.zeros_like(ref) for g in gs]
+        dx = N.pyramid_bwd(*gs, None, B, S, H, L, p, D)
+        return dx[0], dx[1], dx[2], None, None, None, None, None
+
+
+class _GatheredAttnFn(torch.autograd.Function):
+    """Causal attention over rows ``x_cat[b, h, idx[b, h, s]]`` of scorer outputs
+    ``[B, H, S_tot, D]`` (any strides, D contiguous), for scorers from elsewhere."""
+
+    @staticmethod
+    def forward(ctx, q_cat, k_cat, v_cat, idx):
+        B, H, S_tot, D = q_cat.shape
+        assert k_cat.stride() == q_cat.stride() == v_cat.stride(), "scorer outputs must share strides"
+        sb, sh, ss, _ = q_cat.stride()
+        rows = N.Rows(q_cat, k_cat, v_cat, (sb, ss, sh))
+        n = idx.shape[-1]
+        rows.split = S_tot
+        o, lse = N.attn_fwd(rows, idx, B, H, n, D)
+        ctx.save_for_backward(q_cat, k_cat, v_cat, idx, o, lse)
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q_cat, k_cat, v_cat, idx, o, lse = ctx.saved_tensors
+        B, H, S_tot, D = q_cat.shape
+        sb, sh, ss, _ = q_cat.stride()
+        rows = N.Rows(q_cat, k_cat, v_cat, (sb, ss, sh))
+        rows.split = S_tot
+        n = idx.shape[-1]
+        do = do.contiguous()
+        delta = (do.float() * o.float()).sum(-1)
+        dqs, dks, dvs = N.attn_bwd(rows, idx, B, H, n, do, lse, delta, D)
+        inv = N.build_inverse(idx, S_tot)
+        # one-level pyramid over S_tot rows: row r receives dsel[inv[r]] (or 0)
+        dq, dk, dv = N.pyramid_bwd(dqs, dks, dvs, inv, B, S_tot, H, 1, 2, D)
+        return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2), None
+
+
+class _ScatterToBaseFn(torch.autograd.Function):
+    """``_ScatterToBaseAutograd`` (``src/lighthouse_selection.py:517-576``), gather-formulated."""
+
+    @staticmethod
+    def forward(ctx, attn_out, indices, N_shard, N_total, num_levels, pooling_factor):
+        _, _, S_tot = N.pyramid_lengths(N_shard, num_levels, pooling_factor)
+        idx = indices.to(torch.int32).contiguous()
+        inv = N.build_inverse(idx, S_tot)
+        out = N.scatter_fwd(attn_out, inv, N_shard, N_total, num_levels, pooling_factor)
+        ctx.save_for_backward(idx)
+        ctx.geo = (N_shard, num_levels, pooling_factor)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        (idx,) = ctx.saved_tensors
+        S, L, p = ctx.geo
+        dattn, _ = N.scatter_bwd(grad_output, idx, None, S, L, p)
+        return dattn, None, None, None, None, None
+
+
+def scatter_to_base_sequence(attn_out, indices_hp, rank_ids_hp, N_shard: int, N_total: int,
+                             num_levels: int, pooling_factor: int):
+    """Fan-out of selected rows onto the base sequence (``src/lighthouse_selection.py:758-770``).
+
+    Only the single-shard form is built: ``rank_ids_hp`` must be all zeros,
+    which is what every reference caller passes (:817, :1045-1046)."""
+    if rank_ids_hp is not None and bool((rank_ids_hp != 0).any()):
+        raise NotImplementedError("non-zero rank_ids (sharded fan-out) belong to the context-parallel path, "
+                                  "which this single-GPU build does not include")
+    return _ScatterToBaseFn.apply(attn_out, indices_hp, N_shard, N_total, num_levels, pooling_factor)
+
+
+# ---------------------------------------------------------------------------
+# modules
+# ---------------------------------------------------------------------------
+class DialatedLighthouseNormScorer(nn.Module):
+    """Norm scorer (``src/lighthouse_selection.py:578-616``).  Calling it returns the
+    reference's 5-tuple; ``LighthouseLocal`` uses the fused native path instead."""
+
+    def __init__(self, pooling_factor: int = 4, levels: int = 3):
+        super().__init__()
+        self.pooling_factor = pooling_factor
+        self.levels = levels
+
+    dilation = 0
+
+    def forward(self, xq, xk, xv):
+        return _PyramidCatFn.apply(xq, xk, xv, self.levels, self.pooling_factor, 0)
+
+
+class DilatedLighthouseScorer(nn.Module):
+    """Dilated scorer (``src/lighthouse_selection.py:618-689``).
+
+    ``attention=None`` (default) uses the native causal kernel with a fused
+    norm epilogue; a callable is used as in the reference.  ``head_dim`` is
+    accepted for the reference builder's call (``lighthouse-attention.patch:623-628``)."""
+
+    def __init__(self, attention=None, dilation: int = 4, pooling_factor: int = 4, levels: int = 3,
+                 head_dim: int | None = None):
+        super().__init__()
+        self.dilation = dilation
+        self.pooling_factor = pooling_factor
+        self.levels = levels
+        self.attention = attention
+        self.head_dim = head_dim
+
+    def forward(self, xq, xk, xv):
+        if self.attention is None:
+            return _PyramidCatFn.apply(xq, xk, xv, self.levels, self.pooling_factor, self.dilation)
+        return self._forward_with_attention(xq, xk, xv)
+
+    def _forward_with_attention(self, xq, xk, xv):
+        b, s, h, d = xq.shape
+        dil = self.dilation
+
+        def virt(x):
+            return x.reshape(b, s // dil, dil * h, d).transpose(1, 2)
+
+        with torch.no_grad():  # scores only feed the (non-differentiable) selection
+            out_qk = self.attention(virt(xq), virt(xk), virt(xv)).transpose(1, 2).reshape(b, s, h, d)
+            out_kq = self.attention(virt(xk), virt(xq), virt(xv)).transpose(1, 2).reshape(b, s, h, d)
+            sqk = out_qk.norm(dim=-1).transpose(1, 2).float()
+            skq = out_kq.norm(dim=-1).transpose(1, 2).float()
+        return _PyramidCatFn.apply(xq, xk, xv, self.levels, self.pooling_factor, 0, sqk, skq)
+
+
+class DilatedLighthouseGLAScorer(nn.Module):
+    """Name kept for the reference's imports (``src/lighthouse_selection.py:692-755``).
+    The GLA scorer needs the ``fla`` package and is not part of this build."""
+
+    def __init__(self, head_dim: int, dilation: int = 4, pooling_factor: int = 4, levels: int = 3):
+        super().__init__()
+        self.head_dim = head_dim
+        self.dilation = dilation
+        self.pooling_factor = pooling_factor
+        self.levels = levels
+        self.scaling = 1.0 / math.sqrt(head_dim)
+
+    def forward(self, xq, xk, xv, gk):
+        raise RuntimeError("lighthouse_scorer='gla' requires the `fla` package, which this MI355X build does "
+                           "not include; use 'norm' or 'dilated'.")
+
+
+class LighthouseLocal(nn.Module):
+    """Selection attention layer (``src/lighthouse_selection.py:772-825``).
+
+    ``forward(xq, xk, xv)`` takes ``[B, S, H, D]`` bf16 and returns ``[B, H, S, D]``."""
+
+    def __init__(self, attention, scorer, num_levels: int = 3, pooling_factor: int = 4, topk: int = 1024,
+                 tie_break: str = "reference", strict: bool = True, use_native_attention: bool = True):
+        super().__init__()
+        self.scorer = scorer
+        self.num_levels = num_levels
+        self.pooling_factor = pooling_factor
+        self.topk = topk
+        self.attention = attention
+        self.tie_break = tie_break
+        self.strict = strict
+        self.use_native_attention = use_native_attention
+        self.last_indices = None
+
+    def _native_dilation(self):
+        sc = self.scorer
+        if type(sc) is DialatedLighthouseNormScorer:
+            return 0
+        if type(sc) is DilatedLighthouseScorer and sc.attention is None:
+            return sc.dilation
+        return None
+
+    def forward(self, xq, xk, xv):
+        _, s, _, d = xq.shape
+        dil = self._native_dilation()
+        if self.use_native_attention and dil is not None and \
+                self.scorer.levels == self.num_levels and self.scorer.pooling_factor == self.pooling_factor:
+            out, idx = lighthouse_layer(xq, xk, xv, self.num_levels, self.pooling_factor, self.topk,
+                                        self.tie_break, self.strict, dil)
+            self.last_indices = idx
+            return out
+        # generic composition, as in the reference, for scorers and attentions from elsewhere
+        sqk, skq, xq_cat, xk_cat, xv_cat = self.scorer(xq, xk, xv)
+        with torch.no_grad():
+            idx = LighthouseSelectionQkKqChunkedTopkHip.forward(
+                sqk.to(torch.float32), skq.to(torch.float32), self.num_levels, self.pooling_factor, self.topk, s,
+                tie_break=self.tie_break, strict=self.strict)
+        self.last_indices = idx
+        if self.use_native_attention:
+            attn_out = _GatheredAttnFn.apply(xq_cat, xk_cat, xv_cat, idx)
+        else:
+            gi = idx.long().unsqueeze(-1).expand(-1, -1, -1, d)
+            attn_out = self.attention(torch.gather(xq_cat, 2, gi), torch.gather(xk_cat, 2, gi),
+                                      torch.gather(xv_cat, 2, gi))
+        return scatter_to_base_sequence(attn_out, idx, None, s, s, self.num_levels, self.pooling_factor)
+
+
+class DialatedLighthouseNormScorerCP(nn.Module):
+    """Name kept for the reference's imports (``src/lighthouse_selection.py:943-982``);
+    context parallelism is not part of this single-GPU build."""
+
+    def __init__(self, pooling_factor: int = 4, levels: int = 3):
+        super().__init__()
+        self.pooling_factor = pooling_factor
+        self.levels = levels
+
+    def forward(self, xq, xk, xv):
+        raise NotImplementedError("context-parallel Lighthouse is not part of this single-GPU build")
+
+
+class LighthouseCP(nn.Module):
+    """Name kept for the reference's imports (``src/lighthouse_selection.py:985-1054``)."""
+
+    def __init__(self, attention, scorer, num_levels: int = 3, pooling_factor: int = 4, topk: int = 1024):
+        super().__init__()
+        self.scorer = scorer
+        self.num_levels = num_levels
+        self.pooling_factor = pooling_factor
+        self.topk = topk
+        self.attention = attention
+        self._rank, self._world_size, self._cp_group = 0, 1, None
+
+    def set_cp_info(self, rank: int, world_size: int, cp_group):
+        self._rank, self._world_size, self._cp_group = rank, world_size, cp_group
+
+    def forward(self, xq, xk, xv):
+        raise NotImplementedError("context-parallel Lighthouse is not part of this single-GPU build")
