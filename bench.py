@@ -1,0 +1,198 @@
+"""Lighthouse layer forward+backward throughput on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload cfg2] [--no-cpu-baseline]
+
+A step is one forward + backward of one Lighthouse layer (norm scorer) over one
+batch of seeded synthetic N(0,1) bf16 tensors already resident in HBM:
+pyramid + scores -> top-k selection -> gathered causal attention -> fan-out,
+then fan-out adjoint -> attention backward -> pyramid backward.
+
+Prints one JSON line.  `value` is tokens/s = B*S*steps / timed seconds.
+`roofline` is for the kernel with the largest share of the step, timed with
+HIP events recorded on the launch stream between consecutive native ops inside
+the timed region.  `cpu_baseline` times the CPU oracle (a restatement of the
+reference path, fp32) on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Lighthouse layer fwd+bwd tokens/s at S=32K,k=2048 bf16; % HBM/MFMA roofline"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+WORKLOADS = {
+    # name: (B, H, S, L, p, topk, strict)
+    "cfg2": (1, 8, 32768, 3, 4, 2048, True),
+    "cfg3_k1536": (1, 8, 65536, 3, 4, 1536, False),
+    "cfg3_k3072": (1, 8, 65536, 3, 4, 3072, False),
+    "cfg3_k6144": (1, 8, 65536, 3, 4, 6144, False),
+    "cfg5_layer": (1, 8, 32768, 3, 4, 1536, False),
+}
+D = 128
+
+
+def algorithmic_work(B, H, S, L, p, S_sel):
+    """Per-launch algorithmic work of each native op: (kind, amount) with kind
+    'bytes' (HBM-bound) or 'flop' (MFMA-bound).  bf16 = 2 bytes, fp32 = 4."""
+    S_tot = sum(S // p ** l for l in range(L))
+    pairs = S_sel * (S_sel + 1) / 2 * B * H  # causal (query, key) pairs
+    e = 2
+    return {
+        "pyramid": ("bytes", 3 * S * H * D * e * B + 3 * (S_tot - S) * H * D * e * B + 2 * S_tot * H * 4 * B),
+        "select": ("bytes", (2 * S_sel * H * 4 + S_sel * H * 4 + S_tot * H * 4) * B),
+        "attn_fwd": ("flop", 4 * D * pairs),            # S = Q K^T and O = P V
+        "scatter_fwd": ("bytes", ((S_sel + S) * H * D * e + S_tot * H * 4) * B),
+        "scatter_bwd": ("bytes", ((S_sel + S) * H * D * e + S_sel * H * D * e + S_sel * H * 4 * 2) * B),
+        "attn_bwd_dkdv": ("flop", 8 * D * pairs),       # S, dP, dV, dK passes
+        "attn_bwd_dq": ("flop", 2 * D * pairs),         # the dQ pass (S and dP are recomputed)
+        "pyramid_bwd": ("bytes", (3 * S_sel * H * D * e + 3 * S * H * D * e + S_tot * H * 4) * B),
+    }
+
+
+def run_gpu(args, pkg, torch):
+    B, H, S, L, p, k, strict = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(1234)
+    xs = [torch.randn(B, S, H, D, device=dev, generator=g).bfloat16().requires_grad_() for _ in range(3)]
+    dout = torch.randn(B, H, S, D, device=dev, generator=g).bfloat16()
+    scorer = pkg.DialatedLighthouseNormScorer(pooling_factor=p, levels=L)
+    layer = pkg.LighthouseLocal(attention=None, scorer=scorer, num_levels=L, pooling_factor=p, topk=k,
+                                strict=strict)
+    S_sel = pkg._native.geometry(S, L, p, k, strict)[3]
+
+    def step():
+        for x in xs:
+            x.grad = None
+        out = layer(*xs)
+        out.backward(dout)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    marks = []
+
+    def hook(name):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        marks.append((name, ev))
+
+    sel_mod = pkg.lighthouse_selection
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    sel_mod.set_op_hook(hook)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    sel_mod.set_op_hook(None)
+
+    ms_step = start.elapsed_time(end) / args.steps
+    wall_ms_step = (t1 - t0) * 1e3 / args.steps
+    per_op = {}
+    prev = None
+    for name, ev in marks:
+        if name.endswith("_start"):
+            prev = ev
+            continue
+        per_op.setdefault(name, []).append(prev.elapsed_time(ev))
+        prev = ev
+    work = algorithmic_work(B, H, S, L, p, S_sel)
+    kernels = {}
+    for name, ts in per_op.items():
+        avg_ms = sum(ts) / len(ts)
+        kind, amount = work[name]
+        if kind == "flop":
+            ach, peak, unit = amount / (avg_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
+        else:
+            ach, peak, unit = amount / (avg_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+        kernels[name] = {"ms": round(avg_ms, 4), "achieved": round(ach, 2), "unit": unit,
+                         "frac": round(ach / peak, 4), "work": amount}
+    dom = max(kernels, key=lambda n: kernels[n]["ms"])
+    kd = kernels[dom]
+    roofline = {"kernel": dom, "bound": "mfma" if kd["unit"] == "TFLOP/s" else "hbm",
+                "achieved": kd["achieved"], "peak": BF16_PEAK_TFLOPS if kd["unit"] == "TFLOP/s" else HBM_PEAK_GBS,
+                "unit": kd["unit"], "frac": kd["frac"], "traffic": None}
+    tokens_per_s = B * S / (ms_step * 1e-3)
+    cfg = {"workload": f"lighthouse_layer_fwd_bwd_{args.workload}", "B": B, "H": H, "D": D, "S": S,
+           "num_levels": L, "pooling_factor": p, "topk": k, "scorer": "norm", "S_sel": S_sel,
+           "strict": strict, "parallelism": "single GPU"}
+    return {
+        "tokens_per_s": tokens_per_s, "ms_step": ms_step, "wall_ms_step": wall_ms_step, "config": cfg,
+        "roofline": roofline, "kernels": kernels,
+    }
+
+
+def run_cpu_baseline(args, torch):
+    """CPU oracle (fp32, reference path restated) on a bounded sample: the same
+    workload with `--cpu-heads` of its H heads, scaled to all heads."""
+    import numpy as np
+    from oracle import lh_oracle as O
+    B, H, S, L, p, k, strict = WORKLOADS[args.workload]
+    hs = max(1, min(args.cpu_heads, H))
+    g = torch.Generator().manual_seed(99)
+    xs = [torch.randn(B, S, hs, D, generator=g).bfloat16().float().requires_grad_() for _ in range(3)]
+    dout = torch.randn(B, hs, S, D, generator=g)
+    t0 = time.perf_counter()
+    out, idx = O.lighthouse_layer(*xs, L, p, k, strict=strict)
+    out.backward(dout)
+    dt = time.perf_counter() - t0
+    tok_s = B * S / (dt * H / hs)
+    return {"value": round(tok_s, 2), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle layer fwd+bwd fp32 on {hs} of {H} heads (B={B}, S={S}), {dt:.1f} s, "
+                      f"scaled x{H // hs} to all heads"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-heads", type=int, default=4)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU per process and has no multi-GPU path; "
+              f"--gpus {args.gpus} is not supported (use --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import __graft_entry__ as G
+    pkg = G.load_package()
+    r = run_gpu(args, pkg, torch)
+    cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, torch)
+    line = {
+        "metric": METRIC,
+        "value": round(r["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) bf16 q/k/v [B,S,H,D] and upstream grad [B,H,S,D], resident in HBM",
+        "config": r["config"],
+        "roofline": r["roofline"],
+        "cpu_baseline": cpu,
+        "kernels": r["kernels"],
+        "wall_ms_per_step": round(r["wall_ms_step"], 4),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

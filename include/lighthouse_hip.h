@@ -138,6 +138,22 @@ int lh_attn_bwd(const void *q, const void *k, const void *v, int64_t sb, int64_t
                 void *dq, void *dk, void *dv, void *stream);
 
 /*
+ * The two independent halves of lh_attn_bwd (same arguments), for callers that
+ * schedule them separately, e.g. on two streams: the key-stationary dK/dV
+ * kernel and the query-stationary dQ kernel.
+ */
+int lh_attn_bwd_dkdv(const void *q, const void *k, const void *v, int64_t sb, int64_t ss, int64_t sh,
+                     const void *qp, const void *kp, const void *vp, int64_t pb, int64_t ps, int64_t ph,
+                     int split, const int32_t *indices, int B, int H, int n, int D, float scale,
+                     const void *dout, const float *lse, const float *delta,
+                     void *dk, void *dv, void *stream);
+int lh_attn_bwd_dq(const void *q, const void *k, const void *v, int64_t sb, int64_t ss, int64_t sh,
+                   const void *qp, const void *kp, const void *vp, int64_t pb, int64_t ps, int64_t ph,
+                   int split, const int32_t *indices, int B, int H, int n, int D, float scale,
+                   const void *dout, const float *lse, const float *delta,
+                   void *dq, void *stream);
+
+/*
  * Fan-out of each selected row onto the base positions it stands for:
  * out[b,h,t] = sum over levels l of attn[b,h,inverse[b,h,off_l + (t+1)/c_l - 1]].
  * Replaces _scatter_fanout_fwd_kernel / _ScatterToBaseAutograd.forward

@@ -45,6 +45,10 @@ _SIGS = {
                          _I, _I, _I, _I, _F, _P, _P, _P]),
     "lh_attn_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _I, _P,
                          _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P]),
+    "lh_attn_bwd_dkdv": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _I, _P,
+                              _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P]),
+    "lh_attn_bwd_dq": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _I, _P,
+                            _I, _I, _I, _I, _F, _P, _P, _P, _P, _P]),
     "lh_scatter_fwd": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_scatter_bwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_pyramid_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
@@ -246,6 +250,36 @@ def attn_fwd(rows: Rows, indices, B: int, H: int, n: int, D: int = D_SUPPORTED, 
         rc = lib().lh_attn_fwd(*rows.args(), _ptr(idx), B, H, n, D, scale, _ptr(out), _ptr(lse), _stream(dev))
     _check(rc, "lh_attn_fwd")
     return out, lse
+
+
+def attn_bwd_dkdv(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D: int = D_SUPPORTED,
+                  scale: float | None = None):
+    """dK, dV of the gathered rows (key-stationary kernel): two bf16 [B, H, n, D]."""
+    _need_gpu(rows.q, dout)
+    dev = rows.q.device
+    scale = D ** -0.5 if scale is None else scale
+    idx = indices.contiguous() if indices is not None else None
+    dk, dv = (torch.empty(B, H, n, D, dtype=torch.bfloat16, device=dev) for _ in range(2))
+    with torch.cuda.device(dev):
+        rc = lib().lh_attn_bwd_dkdv(*rows.args(), _ptr(idx), B, H, n, D, scale, _ptr(dout.contiguous()),
+                                    _ptr(lse), _ptr(delta), _ptr(dk), _ptr(dv), _stream(dev))
+    _check(rc, "lh_attn_bwd_dkdv")
+    return dk, dv
+
+
+def attn_bwd_dq(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D: int = D_SUPPORTED,
+                scale: float | None = None):
+    """dQ of the gathered rows (query-stationary kernel): bf16 [B, H, n, D]."""
+    _need_gpu(rows.q, dout)
+    dev = rows.q.device
+    scale = D ** -0.5 if scale is None else scale
+    idx = indices.contiguous() if indices is not None else None
+    dq = torch.empty(B, H, n, D, dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib().lh_attn_bwd_dq(*rows.args(), _ptr(idx), B, H, n, D, scale, _ptr(dout.contiguous()),
+                                  _ptr(lse), _ptr(delta), _ptr(dq), _stream(dev))
+    _check(rc, "lh_attn_bwd_dq")
+    return dq
 
 
 def attn_bwd(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D: int = D_SUPPORTED,

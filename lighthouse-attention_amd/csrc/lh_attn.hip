@@ -618,24 +618,57 @@ extern "C" int lh_attn_fwd(const void* q, const void* k, const void* v, int64_t 
   return LH_OK;
 }
 
+namespace {
+// parts: bit 0 = dK/dV kernel, bit 1 = dQ kernel
+int attn_bwd_parts(int parts, const void* q, const void* k, const void* v, int64_t sb, int64_t ss, int64_t sh,
+                   const void* qp, const void* kp, const void* vp, int64_t pb, int64_t ps, int64_t ph, int split,
+                   const int32_t* indices, int B, int H, int n, int D, float scale, const void* dout,
+                   const float* lse, const float* delta, void* dq, void* dk, void* dv, void* stream) {
+  AttnArgs a{};
+  int rc = fill_rows(a, q, k, v, sb, ss, sh, qp, kp, vp, pb, ps, ph, split, indices, B, H, n, D, scale);
+  if (rc) return rc;
+  if (!dout || !lse || !delta || !al16(dout)) return LH_ERR_INVALID_ARG;
+  if ((parts & 1) && (!dk || !dv || !al16(dk) || !al16(dv))) return LH_ERR_INVALID_ARG;
+  if ((parts & 2) && (!dq || !al16(dq))) return LH_ERR_INVALID_ARG;
+  a.dout = (const bf16_t*)dout; a.lse_in = lse; a.delta = delta;
+  a.dq = (bf16_t*)dq; a.dk = (bf16_t*)dk; a.dv = (bf16_t*)dv;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (parts & 1) {
+    hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(a.nq * a.BH), dim3(256), 0, st, a);
+    LH_CHECK_LAUNCH();
+  }
+  if (parts & 2) {
+    hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3(a.nq * a.BH), dim3(256), 0, st, a);
+    LH_CHECK_LAUNCH();
+  }
+  return LH_OK;
+}
+}  // namespace
+
 extern "C" int lh_attn_bwd(const void* q, const void* k, const void* v, int64_t sb, int64_t ss, int64_t sh,
                            const void* qp, const void* kp, const void* vp, int64_t pb, int64_t ps, int64_t ph,
                            int split, const int32_t* indices, int B, int H, int n, int D, float scale,
                            const void* dout, const float* lse, const float* delta, void* dq, void* dk, void* dv,
                            void* stream) {
-  AttnArgs a{};
-  int rc = fill_rows(a, q, k, v, sb, ss, sh, qp, kp, vp, pb, ps, ph, split, indices, B, H, n, D, scale);
-  if (rc) return rc;
-  if (!dout || !lse || !delta || !dq || !dk || !dv || !al16(dout) || !al16(dq) || !al16(dk) || !al16(dv))
-    return LH_ERR_INVALID_ARG;
-  a.dout = (const bf16_t*)dout; a.lse_in = lse; a.delta = delta;
-  a.dq = (bf16_t*)dq; a.dk = (bf16_t*)dk; a.dv = (bf16_t*)dv;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(a.nq * a.BH), dim3(256), 0, st, a);
-  LH_CHECK_LAUNCH();
-  hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3(a.nq * a.BH), dim3(256), 0, st, a);
-  LH_CHECK_LAUNCH();
-  return LH_OK;
+  return attn_bwd_parts(3, q, k, v, sb, ss, sh, qp, kp, vp, pb, ps, ph, split, indices, B, H, n, D, scale, dout,
+                        lse, delta, dq, dk, dv, stream);
+}
+
+extern "C" int lh_attn_bwd_dkdv(const void* q, const void* k, const void* v, int64_t sb, int64_t ss, int64_t sh,
+                                const void* qp, const void* kp, const void* vp, int64_t pb, int64_t ps, int64_t ph,
+                                int split, const int32_t* indices, int B, int H, int n, int D, float scale,
+                                const void* dout, const float* lse, const float* delta, void* dk, void* dv,
+                                void* stream) {
+  return attn_bwd_parts(1, q, k, v, sb, ss, sh, qp, kp, vp, pb, ps, ph, split, indices, B, H, n, D, scale, dout,
+                        lse, delta, nullptr, dk, dv, stream);
+}
+
+extern "C" int lh_attn_bwd_dq(const void* q, const void* k, const void* v, int64_t sb, int64_t ss, int64_t sh,
+                              const void* qp, const void* kp, const void* vp, int64_t pb, int64_t ps, int64_t ph,
+                              int split, const int32_t* indices, int B, int H, int n, int D, float scale,
+                              const void* dout, const float* lse, const float* delta, void* dq, void* stream) {
+  return attn_bwd_parts(2, q, k, v, sb, ss, sh, qp, kp, vp, pb, ps, ph, split, indices, B, H, n, D, scale, dout,
+                        lse, delta, dq, nullptr, nullptr, stream);
 }
 
 extern "C" int lh_dilated_scores(const void* xq, const void* xk, const void* xv, float* scores_qk, float* scores_kq,

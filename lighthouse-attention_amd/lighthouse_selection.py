@@ -96,6 +96,24 @@ def _base_rows(xq, xk, xv, pq=None, pk=None, pv=None):
     return N.Rows(xq, xk, xv, (sb, ss, sh), pq, pk, pv, (pb, ps, ph), split=S)
 
 
+_op_hook = None
+
+
+def set_op_hook(fn):
+    """Install ``fn(name)``, called on the host right after each native op of the
+    layer is enqueued (names: ``pyramid``, ``dilated_scores``, ``select``,
+    ``attn_fwd``, ``scatter_fwd``, ``scatter_bwd``, ``attn_bwd_dkdv``,
+    ``attn_bwd_dq``, ``pyramid_bwd``) and with ``fwd_start`` / ``bwd_start``
+    before the first one; e.g. to record a stream event per op.  ``None`` removes it."""
+    global _op_hook
+    _op_hook = fn
+
+
+def _mark(name):
+    if _op_hook is not None:
+        _op_hook(name)
+
+
 class _LighthouseLayerFn(torch.autograd.Function):
     """Whole layer: pyramid -> selection -> gathered causal attention -> fan-out.
 
@@ -109,28 +127,43 @@ class _LighthouseLayerFn(torch.autograd.Function):
         xq, xk, xv = xq.contiguous(), xk.contiguous(), xv.contiguous()
         lens, offs, S_tot = N.pyramid_lengths(S, L, p)
         _, _, _, S_sel = N.geometry(S, L, p, topk, strict)
+        _mark("fwd_start")
         if dilation:
             scores = N.dilated_scores(xq, xk, xv, dilation, S_tot)
+            _mark("dilated_scores")
             pq, pk, pv, sqk, skq = N.pyramid_fwd(xq, xk, xv, L, p, scores=scores)
         else:
             pq, pk, pv, sqk, skq = N.pyramid_fwd(xq, xk, xv, L, p)
+        _mark("pyramid")
         idx, inv = N.select_topk(sqk, skq, S, L, p, topk, tie=tie, strict=strict)
+        _mark("select")
         rows = _base_rows(xq, xk, xv, pq, pk, pv)
         o, lse = N.attn_fwd(rows, idx, B, H, S_sel, D)
+        _mark("attn_fwd")
         out = N.scatter_fwd(o, inv, S, S, L, p)
+        _mark("scatter_fwd")
         ctx.save_for_backward(xq, xk, xv, pq, pk, pv, idx, inv, o, lse)
         ctx.geo = (B, S, H, D, L, p, S_sel)
         ctx.mark_non_differentiable(idx)
+        ctx.set_materialize_grads(False)  # no zero-filled gradient for the index output
         return out, idx
 
     @staticmethod
     def backward(ctx, dout, _didx):
         xq, xk, xv, pq, pk, pv, idx, inv, o, lse = ctx.saved_tensors
         B, S, H, D, L, p, S_sel = ctx.geo
+        if dout is None:
+            return None, None, None, None, None, None, None, None, None
+        _mark("bwd_start")
         dattn, delta = N.scatter_bwd(dout, idx, o, S, L, p)
+        _mark("scatter_bwd")
         rows = _base_rows(xq, xk, xv, pq, pk, pv)
-        dqs, dks, dvs = N.attn_bwd(rows, idx, B, H, S_sel, dattn, lse, delta, D)
+        dks, dvs = N.attn_bwd_dkdv(rows, idx, B, H, S_sel, dattn, lse, delta, D)
+        _mark("attn_bwd_dkdv")
+        dqs = N.attn_bwd_dq(rows, idx, B, H, S_sel, dattn, lse, delta, D)
+        _mark("attn_bwd_dq")
         dxq, dxk, dxv = N.pyramid_bwd(dqs, dks, dvs, inv, B, S, H, L, p, D)
+        _mark("pyramid_bwd")
         return dxq, dxk, dxv, None, None, None, None, None, None
 
 
@@ -192,13 +225,18 @@ class _GatheredAttnFn(torch.autograd.Function):
     ``[B, H, S_tot, D]`` (any strides, D contiguous), for scorers from elsewhere."""
 
     @staticmethod
-    def forward(ctx, q_cat, k_cat, v_cat, idx):
-        B, H, S_tot, D = q_cat.shape
+    def _rows(q_cat, k_cat, v_cat):
+        # every row lives in the one [B, H, S_tot, D] tensor: rows >= split never occur
         assert k_cat.stride() == q_cat.stride() == v_cat.stride(), "scorer outputs must share strides"
         sb, sh, ss, _ = q_cat.stride()
-        rows = N.Rows(q_cat, k_cat, v_cat, (sb, ss, sh))
+        st = (sb, ss, sh)
+        return N.Rows(q_cat, k_cat, v_cat, st, q_cat, k_cat, v_cat, st, split=q_cat.shape[2])
+
+    @staticmethod
+    def forward(ctx, q_cat, k_cat, v_cat, idx):
+        B, H, S_tot, D = q_cat.shape
+        rows = _GatheredAttnFn._rows(q_cat, k_cat, v_cat)
         n = idx.shape[-1]
-        rows.split = S_tot
         o, lse = N.attn_fwd(rows, idx, B, H, n, D)
         ctx.save_for_backward(q_cat, k_cat, v_cat, idx, o, lse)
         return o
@@ -207,9 +245,7 @@ class _GatheredAttnFn(torch.autograd.Function):
     def backward(ctx, do):
         q_cat, k_cat, v_cat, idx, o, lse = ctx.saved_tensors
         B, H, S_tot, D = q_cat.shape
-        sb, sh, ss, _ = q_cat.stride()
-        rows = N.Rows(q_cat, k_cat, v_cat, (sb, ss, sh))
-        rows.split = S_tot
+        rows = _GatheredAttnFn._rows(q_cat, k_cat, v_cat)
         n = idx.shape[-1]
         do = do.contiguous()
         delta = (do.float() * o.float()).sum(-1)

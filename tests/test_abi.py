@@ -1,0 +1,127 @@
+"""C-ABI and host-logic checks that need no GPU.
+
+The library must load and export every entry point declared in
+include/lighthouse_hip.h; host-side geometry and argument validation run
+without launching anything; the Python API exposes the names the reference's
+model wiring imports (lighthouse-attention.patch:591-598).
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import lh_oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "lighthouse_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lh_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    for n in ["lh_pyramid_fwd", "lh_select_topk", "lh_attn_fwd", "lh_attn_bwd", "lh_scatter_fwd",
+              "lh_scatter_bwd", "lh_pyramid_bwd", "lh_dilated_scores", "lh_select_geometry"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg._native.lib()
+    for n in _declared():
+        assert hasattr(lib, n), f"{n} declared in the header but not exported"
+    assert set(_declared()) == set(pkg._native.EXPORTED)
+    assert lib.lh_abi_version() == 1
+
+
+def test_strerror(pkg):
+    lib = pkg._native.lib()
+    for rc in range(5):
+        assert lib.lh_strerror(rc)
+    assert b"unknown" in lib.lh_strerror(99)
+
+
+@pytest.mark.parametrize("geo", [(32768, 3, 4, 2048), (4096, 3, 4, 256), (4096, 3, 4, 1536), (65536, 3, 4, 1536),
+                                 (65536, 3, 4, 3072), (65536, 3, 4, 6144), (131072, 5, 2, 1536),
+                                 (32768, 3, 4, 1536), (5000, 3, 4, 256), (2048, 2, 2, 128), (98304, 3, 4, 4096)])
+def test_geometry_matches_oracle(pkg, geo):
+    S, L, p, k = geo
+    g = O.tile_geometry(S, L, p, k)
+    T, NCC, per_tile, S_sel = pkg._native.geometry(S, L, p, k, strict=False)
+    assert (T, NCC, per_tile, S_sel) == (g.T, g.NCC, g.per_tile, g.S_sel)
+    if g.strict_ok:
+        assert pkg._native.geometry(S, L, p, k, strict=True)[3] == g.S_sel
+        assert g.S_sel == pkg.compute_output_indices_selection(S, L, p, k)
+    else:
+        with pytest.raises(AssertionError):
+            pkg._native.geometry(S, L, p, k, strict=True)
+
+
+def test_host_validation_rejects_before_launch(pkg):
+    lib = pkg._native.lib()
+    null = ctypes.c_void_p(0)
+    # unsupported head dim, null pointers, bad tie mode: all refused on the host
+    assert lib.lh_attn_fwd(null, null, null, 0, 0, 0, null, null, null, 0, 0, 0, 0, null,
+                           1, 1, 128, 64, ctypes.c_float(0.1), null, null, null) == 4
+    assert lib.lh_attn_fwd(null, null, null, 0, 0, 0, null, null, null, 0, 0, 0, 0, null,
+                           1, 1, 128, 128, ctypes.c_float(0.1), null, null, null) == 1
+    assert lib.lh_select_topk(null, null, null, null, 1, 1, 4096, 3, 4, 256, 0, 1, null) == 1
+    assert lib.lh_pyramid_fwd(null, null, null, 0, 0, 0, null, null, null, 0, 0, 0, null, null,
+                              1, 1024, 1, 128, 3, 4, 0, null) == 1
+    assert lib.lh_scatter_fwd(null, null, null, 1, 1, 1024, 1024, 10, 64, 3, 4, null) == 4
+    assert lib.lh_pyramid_bwd(null, null, null, 0, 0, 0, null, null, null, null, 1, 1024, 1, 128, 3, 3,
+                              null) == 1
+    assert lib.lh_select_geometry(4096, 3, 4, 1536, 1, None, None, None, None) == 2
+    assert lib.lh_select_geometry(4096, 1, 4, 256, 0, None, None, None, None) == 1
+
+
+def test_no_cpu_fallback(pkg):
+    x = torch.zeros(1, 256, 1, 128, dtype=torch.bfloat16)
+    with pytest.raises(pkg._native.LighthouseHipError):
+        pkg._native.pyramid_fwd(x, x, x, 2, 2)
+    with pytest.raises(pkg._native.LighthouseHipError):
+        pkg.lighthouse_layer(x, x, x, num_levels=2, pooling_factor=2, topk=128)
+
+
+def test_product_code_does_not_import_the_oracle():
+    pkg_dir = os.path.join(ROOT, "lighthouse-attention_amd")
+    for dirpath, _, files in os.walk(pkg_dir):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".cpp")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert not re.search(r"^\s*(from|import)\s+oracle", text, flags=re.M), f
+                assert "select_ref" not in text and "lh_oracle" not in text, f
+
+
+def test_reference_import_names_and_constructors(pkg):
+    for name in ["DilatedLighthouseScorer", "DialatedLighthouseNormScorer", "DilatedLighthouseGLAScorer",
+                 "LighthouseLocal", "DialatedLighthouseNormScorerCP", "LighthouseCP"]:
+        assert hasattr(pkg, name)
+    norm = pkg.DialatedLighthouseNormScorer(pooling_factor=4, levels=3)
+    dil = pkg.DilatedLighthouseScorer(head_dim=128, dilation=4, pooling_factor=4, levels=3)
+    assert dil.attention is None and dil.dilation == 4
+    layer = pkg.LighthouseLocal(scorer=norm, num_levels=3, pooling_factor=4, topk=2048, attention=None)
+    assert layer.topk == 2048 and layer.tie_break == "reference" and layer.strict
+    gla = pkg.DilatedLighthouseGLAScorer(head_dim=128)
+    with pytest.raises(RuntimeError, match="fla"):
+        gla(None, None, None, None)
+    cp = pkg.LighthouseCP(attention=None, scorer=pkg.DialatedLighthouseNormScorerCP())
+    cp.set_cp_info(0, 2, None)
+    with pytest.raises(NotImplementedError):
+        cp(None, None, None)
+    assert pkg.compute_output_indices_selection(32768, 3, 4, 2048) == 18432
+    assert pkg.LighthouseSelectionQkKqChunkedTopkNvrtc is pkg.LighthouseSelectionQkKqChunkedTopkHip
+
+
+def test_selection_class_asserts_like_reference(pkg):
+    s = torch.zeros(1, 1, 5376)
+    with pytest.raises(AssertionError):  # not on a GPU
+        pkg.LighthouseSelectionQkKqChunkedTopkNvrtc.forward(s, s, 3, 4, 256, 4096)
+    with pytest.raises(AssertionError):
+        pkg.LighthouseSelectionQkKqChunkedTopkNvrtc.forward(s, s[..., :10], 3, 4, 256, 4096)

@@ -98,12 +98,3 @@ def test_local_module_api(pkg, dev):
     out2.backward(dout.to(dev))
     for n, g1, x in zip("qkv", grads, xs2):
         assert_close(x.grad, g1.float(), f"generic path d{n}", max_abs=1e-2, rel_l2=4e-3)
-
-
-def test_reference_import_names(pkg):
-    for name in ["DilatedLighthouseScorer", "DialatedLighthouseNormScorer", "DilatedLighthouseGLAScorer",
-                 "LighthouseLocal", "DialatedLighthouseNormScorerCP", "LighthouseCP"]:
-        assert hasattr(pkg, name)
-    # the reference builder's dilated call (lighthouse-attention.patch:623-628) constructs
-    sc = pkg.DilatedLighthouseScorer(head_dim=128, dilation=4, pooling_factor=4, levels=3)
-    assert sc.dilation == 4 and sc.attention is None
