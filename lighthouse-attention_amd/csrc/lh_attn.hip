@@ -12,13 +12,23 @@
 //     l^32, and the per-query rescale of O is a per-lane scalar.
 //   * The exp'd scores feed P V directly from registers: the C-layout of S^T
 //     (key = 8*(v/4) + 4*(l/32) + v%4) is used as the k-order of the next MFMA,
-//     and V is staged transposed in LDS so the A operand reads the same key
-//     order (two 8-byte LDS reads per operand).
+//     and the A operand V^T is read from the row-major V tile with the
+//     transposing LDS read ds_read_b64_tr_b16 in the same key order.
+//   * LDS tiles are row-major, unpadded and XOR-swizzled per 16-byte chunk, and
+//     are filled by direct global->LDS loads (global_load_lds_dwordx4): no
+//     register staging, no transposed copies.  Two buffers per operand; the
+//     next tile's loads are issued before the current tile's MFMAs.
 //   * Rows are gathered on the fly: row s of (b, h) is read through
 //     indices[b, h, s] from the base [B, S, H, D] tensor or the pooled
-//     [B, Sp, H, D] tensor; nothing is materialised.
-//   * K/V tiles are double-buffered in LDS; the next tile's global loads are
-//     issued before the current tile's MFMAs.
+//     [B, Sp, H, D] tensor (32-bit element offsets within one (b, h); K and V
+//     share them).  Rows past the end are clamped to the last row and masked,
+//     so loads never branch.
+//   * One tile body serves masked and unmasked tiles (a wave-uniform flag
+//     guards the mask code), so accumulators keep one register assignment.
+//   * The running maximum is only raised when a row's maximum grows by more
+//     than 2^8 (in exp2 units); until then exp'd scores may reach 2^8, which
+//     bf16 and fp32 hold exactly as well as values <= 1, and the O rescale is
+//     skipped.
 //   * Backward is deterministic: dK/dV in a key-stationary kernel, dQ in a
 //     query-stationary kernel, no atomics.
 // Softmax runs in the exp2 domain with scale*log2(e); the stored LSE is
@@ -29,8 +39,7 @@ namespace {
 
 constexpr int BM = 128;  // queries (or keys) per workgroup: 4 waves x 32
 constexpr int BN = 64;   // rows per LDS tile
-constexpr int RS = 136;  // row-major tile stride in bf16 (128 + 8 pad)
-constexpr int TS = 68;   // transposed tile stride in bf16 (64 + 4 pad)
+constexpr float RESCALE_LOG2 = 8.0f;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -61,6 +70,34 @@ struct AttnArgs {
   bf16_t *dq, *dk, *dv;
 };
 
+// Row source of one (b, h): uniform base pointers and 32-bit strides.
+struct BhRows {
+  const bf16_t *q, *k, *v, *qp, *kp, *vp;
+  const int32_t* idx;
+  int ss, ps, split, last;
+};
+
+__device__ __forceinline__ BhRows bh_rows(const AttnArgs& a, int bh) {
+  const Rows& R = a.R;
+  const int b = bh / a.H, h = bh % a.H;
+  BhRows m;
+  const int64_t ob = (int64_t)b * R.sb + (int64_t)h * R.sh;
+  const int64_t op = (int64_t)b * R.pb + (int64_t)h * R.ph;
+  m.q = R.q + ob; m.k = R.k + ob; m.v = R.v + ob;
+  m.qp = R.qp + op; m.kp = R.kp + op; m.vp = R.vp + op;
+  m.idx = R.idx ? R.idx + (int64_t)bh * a.n : nullptr;
+  m.ss = (int)R.ss; m.ps = (int)R.ps; m.split = R.split; m.last = a.n - 1;
+  return m;
+}
+
+// element offset of selected row s (clamped to the last row); `pooled` picks the tensor
+__device__ __forceinline__ uint32_t row_off(const BhRows& m, int s, bool& pooled) {
+  s = min(s, m.last);
+  const int r = m.idx ? m.idx[s] : s;
+  pooled = r >= m.split;
+  return pooled ? (uint32_t)(r - m.split) * (uint32_t)m.ps : (uint32_t)r * (uint32_t)m.ss;
+}
+
 __device__ __forceinline__ floatx16 mfma(const u32x4 a, const u32x4 b, const floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
                                                  0, 0);
@@ -73,17 +110,11 @@ __device__ __forceinline__ uint32_t cvt2(float lo, float hi) {
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// element offset of row s of (b, h); `pooled` tells which tensor holds it
-__device__ __forceinline__ int64_t row_off(const Rows& R, int b, int h, int bh, int n, int s, bool& pooled) {
-  const int r = R.idx ? R.idx[(int64_t)bh * n + s] : s;
-  pooled = r >= R.split;
-  return pooled ? (int64_t)b * R.pb + (int64_t)(r - R.split) * R.ps + (int64_t)h * R.ph
-                : (int64_t)b * R.sb + (int64_t)r * R.ss + (int64_t)h * R.sh;
-}
+__device__ __forceinline__ u32x4 ldg16(const bf16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 // Blocks are dispatched round-robin over the 8 XCDs; give each XCD a
 // contiguous run of (b, h) so K/V rows stay in that XCD's L2, and run the
-// heaviest (latest) query blocks first.
+// heaviest causal blocks first.
 __device__ __forceinline__ void schedule(int w, int nblk, int BH, int& bh, int& blk, bool heavy_last) {
   const int total = nblk * BH;
   int t = w;
@@ -93,68 +124,78 @@ __device__ __forceinline__ void schedule(int w, int nblk, int BH, int& bh, int& 
   blk = heavy_last ? (nblk - 1 - r) : r;
 }
 
-// Tile loader: thread owns rows 4*rq .. 4*rq+3 of the tile and 8 columns at 8*dc.
-struct Tile4 {
-  u32x4 r[4];
-};
+// ---------------------------------------------------------------------------
+// LDS tiles: 64 rows x 128 bf16, rows unpadded (256 B), 16-byte chunks
+// swizzled as chunk ^ swz(row).  swz is a bijection on every 16 consecutive
+// rows (so 128-bit row reads of 16 rows at one chunk hit distinct banks) and
+// gives 4 consecutive rows distinct high bits (so the transposing reads of a
+// 4-row x 4-chunk block hit distinct banks).  Tiles are filled by direct
+// global->LDS loads: lane l of a 16-byte load writes LDS base + 16*l, so each
+// lane fetches the logical chunk that the swizzle puts in its slot.
+// ---------------------------------------------------------------------------
+constexpr int TILE = BN * LH_D;  // elements per tile (16 KB)
 
-__device__ __forceinline__ void load_gathered(Tile4& t, const bf16_t* base, const bf16_t* pool, const Rows& R, int b,
-                                              int h, int bh, int n, int row0, int dc) {
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ u32x2 ld_tr16(const bf16_t* p) {
+  const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+__device__ __forceinline__ void g2l16(const bf16_t* g, bf16_t* lds_base) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_base, 16, 0, 0);
+}
+
+// Wave w fills rows 16w .. 16w+15 of one tile (two tiles sharing the row map when
+// tile2 != null) from selected rows row0 .. row0+63: four 1 KB loads of 4 rows.
+__device__ __forceinline__ void issue_gathered(bf16_t* tile, const bf16_t* base, const bf16_t* pool, bf16_t* tile2,
+                                               const bf16_t* base2, const bf16_t* pool2, const BhRows& m, int row0,
+                                               int w, int lane) {
+  const int rsub = lane >> 4, slot = lane & 15;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int s = row0 + i;
-    if (s < n) {
-      bool pooled;
-      const int64_t o = row_off(R, b, h, bh, n, s, pooled);
-      t.r[i] = *reinterpret_cast<const u32x4*>((pooled ? pool : base) + o + 8 * dc);
-    } else {
-      t.r[i] = u32x4{0u, 0u, 0u, 0u};
-    }
+    const int r = 16 * w + 4 * i + rsub;
+    bool pooled;
+    const uint32_t o = row_off(m, row0 + r, pooled) + 8 * (slot ^ swz(r));
+    g2l16((pooled ? pool : base) + o, tile + (16 * w + 4 * i) * LH_D);
+    if (tile2) g2l16((pooled ? pool2 : base2) + o, tile2 + (16 * w + 4 * i) * LH_D);
   }
 }
 
-__device__ __forceinline__ void load_dense(Tile4& t, const bf16_t* base, int n, int row0, int dc) {
+__device__ __forceinline__ void issue_dense(bf16_t* tile, const bf16_t* base, int last, int row0, int w, int lane) {
+  const int rsub = lane >> 4, slot = lane & 15;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int s = row0 + i;
-    t.r[i] = (s < n) ? *reinterpret_cast<const u32x4*>(base + (int64_t)s * LH_D + 8 * dc) : u32x4{0u, 0u, 0u, 0u};
+    const int r = 16 * w + 4 * i + rsub;
+    g2l16(base + (uint32_t)min(row0 + r, last) * LH_D + 8 * (slot ^ swz(r)), tile + (16 * w + 4 * i) * LH_D);
   }
 }
 
-__device__ __forceinline__ void store_rowmajor(const Tile4& t, bf16_t* lds, int rq, int dc) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(lds + (4 * rq + i) * RS + 8 * dc) = t.r[i];
+// every direct load of this wave has landed in LDS
+__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0); }
+
+// A operand from tile row r: d = 16c + 8hh .. 16c + 8hh + 7
+__device__ __forceinline__ u32x4 op_row(const bf16_t* tile, int r, int c, int hh) {
+  return *reinterpret_cast<const u32x4*>(tile + r * LH_D + (((2 * c + hh) ^ swz(r)) << 3));
 }
 
-// lds is [D][TS]: column block of 4 consecutive rows per 8-byte store
-__device__ __forceinline__ void store_transposed(const Tile4& t, bf16_t* lds, int rq, int dc) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int w = e >> 1;
-    uint32_t a0 = t.r[0][w], a1 = t.r[1][w], a2 = t.r[2][w], a3 = t.r[3][w];
-    u32x2 v;
-    if (e & 1) {
-      v.x = (a0 >> 16) | (a1 & 0xffff0000u);
-      v.y = (a2 >> 16) | (a3 & 0xffff0000u);
-    } else {
-      v.x = (a0 & 0xffffu) | (a1 << 16);
-      v.y = (a2 & 0xffffu) | (a3 << 16);
-    }
-    *reinterpret_cast<u32x2*>(lds + (8 * dc + e) * TS + 4 * rq) = v;
-  }
-}
-
-// A operand from a transposed tile: row `d`, 16-column chunk starting at col0,
-// key order 4*hh + {0..3} then 8 + 4*hh + {0..3}
-__device__ __forceinline__ u32x4 ld_tr(const bf16_t* lds, int d, int col0, int hh) {
-  const bf16_t* p = lds + d * TS + col0 + 4 * hh;
-  const u32x2 lo = *reinterpret_cast<const u32x2*>(p);
-  const u32x2 hi = *reinterpret_cast<const u32x2*>(p + 8);
+// A operand of X^T: column d = 32db + lane%32; k-slots u are rows
+// r0 + 8(u/4) + 4(lane/32) + u%4 (r0 a multiple of 16).  Within each 16-lane
+// group, ds_read_b64_tr_b16 returns to lane i, element e, the 16-bit word i%4 of
+// the 8 bytes addressed by lane i/4 + 4e; each lane therefore addresses 4
+// columns of one row of a 4-row x 16-column block.
+__device__ __forceinline__ u32x4 op_tr(const bf16_t* tile, int r0, int db, int lane) {
+  const int g = lane >> 4, j = lane & 15;
+  const int r = r0 + 4 * (lane >> 5) + (j >> 2);
+  const int ch = 4 * db + 2 * (g & 1) + ((j & 3) >> 1);
+  const int sub = (j & 1) << 2;
+  const u32x2 lo = ld_tr16(tile + r * LH_D + ((ch ^ swz(r)) << 3) + sub);
+  const u32x2 hi = ld_tr16(tile + (r + 8) * LH_D + ((ch ^ swz(r + 8)) << 3) + sub);
   return u32x4{lo.x, lo.y, hi.x, hi.y};
-}
-
-__device__ __forceinline__ u32x4 ld_row(const bf16_t* lds, int row, int col) {
-  return *reinterpret_cast<const u32x4*>(lds + row * RS + col);
 }
 
 // 8 fp32 accumulator values v = 8*c2 .. 8*c2+7 -> bf16 B operand
@@ -163,139 +204,155 @@ __device__ __forceinline__ u32x4 pack_frag(const floatx16& s, int c2) {
   return u32x4{cvt2(s[v + 0], s[v + 1]), cvt2(s[v + 2], s[v + 3]), cvt2(s[v + 4], s[v + 5]), cvt2(s[v + 6], s[v + 7])};
 }
 
+// key index held in accumulator slot v of a 32-key block
+__device__ __forceinline__ int slot_key(int v, int hh) { return 8 * (v >> 2) + 4 * hh + (v & 3); }
+
+__device__ __forceinline__ void store_rows_bf16(bf16_t* row, const floatx16 (&acc)[4], float sc, int hh) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      u32x2 w;
+      w.x = cvt2(acc[d][4 * g + 0] * sc, acc[d][4 * g + 1] * sc);
+      w.y = cvt2(acc[d][4 * g + 2] * sc, acc[d][4 * g + 3] * sc);
+      *reinterpret_cast<u32x2*>(row + d * 32 + 8 * g + 4 * hh) = w;
+    }
+  }
+}
+
 // ===========================================================================
 // forward (query-stationary)
 // ===========================================================================
+struct FwdState {
+  floatx16 o[4];
+  float m;  // running max in raw (unscaled) score units
+  float l;  // this lane's half of the row sum
+};
+
+__device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], const bf16_t* Ks, const bf16_t* Vs,
+                                         int k0, int my_q, int n, int lane, float sl2, bool mask) {
+  const int l32 = lane & 31, hh = lane >> 5;
+  floatx16 s[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    s[kb] = mfma(op_row(Ks, kb * 32 + l32, 0, hh), qf[0], floatx16{});
+#pragma unroll
+    for (int c = 1; c < 8; ++c) s[kb] = mfma(op_row(Ks, kb * 32 + l32, c, hh), qf[c], s[kb]);
+  }
+  if (mask) {  // wave-uniform: only tiles that cross the diagonal or the end
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = k0 + kb * 32 + slot_key(v, hh);
+        if (key > my_q || key >= n) s[kb][v] = -INFINITY;
+      }
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const bool raise = mx > st.m + RESCALE_LOG2 / sl2;
+  if (__any(raise)) {
+    const float m_new = raise ? mx : st.m;
+    const float alpha = raise ? ex2((st.m - m_new) * sl2) : 1.f;  // 0 on the first raise (m = -inf)
+    st.l *= alpha;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) st.o[d] *= alpha;
+    st.m = m_new;
+  }
+  const float nm = (st.m == -INFINITY) ? 0.f : -st.m * sl2;
+  float ls = 0.f;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const float p = ex2(fmaf(s[kb][v], sl2, nm));
+      s[kb][v] = p;
+      ls += p;
+    }
+  }
+  st.l += ls;
+  u32x4 pf[2][2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    pf[kb][0] = pack_frag(s[kb], 0);
+    pf[kb][1] = pack_frag(s[kb], 1);
+  }
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) st.o[d] = mfma(op_tr(Vs, kb * 32 + 16 * c2, d, lane), pf[kb][c2], st.o[d]);
+    }
+  }
+}
+
 template <int EPI>  // 0: O + LSE;  1: bf16-rounded row norms of O into `scores`
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16_t Ks[2][BN * RS];
-  __shared__ __attribute__((aligned(16))) bf16_t Vt[2][LH_D * TS];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  __shared__ __attribute__((aligned(1024))) bf16_t lds[4 * TILE];  // K0 K1 V0 V1
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int bh, qb;
   schedule(blockIdx.x, a.nq, a.BH, bh, qb, true);
-  const int b = bh / a.H, h = bh % a.H, n = a.n;
-  const Rows& R = a.R;
+  const int n = a.n;
+  const BhRows m = bh_rows(a, bh);
   const int q0 = qb * BM, qw = q0 + wave * 32, my_q = qw + l32;
 
   u32x4 qf[8];
-  if (my_q < n) {
+  {
     bool pooled;
-    const int64_t o = row_off(R, b, h, bh, n, my_q, pooled);
-    const bf16_t* p = (pooled ? R.qp : R.q) + o + 8 * hh;
+    const uint32_t o = row_off(m, my_q, pooled) + 8 * hh;
+    const bf16_t* p = (pooled ? m.qp : m.q) + o;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) qf[c] = *reinterpret_cast<const u32x4*>(p + 16 * c);
-  } else {
-#pragma unroll
-    for (int c = 0; c < 8; ++c) qf[c] = u32x4{0u, 0u, 0u, 0u};
+    for (int c = 0; c < 8; ++c) qf[c] = ldg16(p + 16 * c);
   }
 
   const int kend = min(q0 + BM, n);
   const int nt = (kend + BN - 1) / BN;
-  const int rq = tid & 15, dc = tid >> 4;
-  Tile4 kr, vr;
-  load_gathered(kr, R.k, R.kp, R, b, h, bh, n, 4 * rq, dc);
-  load_gathered(vr, R.v, R.vp, R, b, h, bh, n, 4 * rq, dc);
-  store_rowmajor(kr, Ks[0], rq, dc);
-  store_transposed(vr, Vt[0], rq, dc);
+  issue_gathered(lds, m.k, m.kp, lds + 2 * TILE, m.v, m.vp, m, 0, wave, lane);
+  wait_loads();
   __syncthreads();
 
-  floatx16 o[4];
+  FwdState st;
 #pragma unroll
-  for (int d = 0; d < 4; ++d) o[d] = floatx16{};
-  float m_i = -INFINITY, l_i = 0.f;
+  for (int d = 0; d < 4; ++d) st.o[d] = floatx16{};
+  st.m = -INFINITY;
+  st.l = 0.f;
+  // tiles whose 64 keys are all <= this wave's first query and < n need no mask
+  const int nfull = min((qw + 1) / BN, n / BN);
 
   for (int j = 0; j < nt; ++j) {
     const int cur = j & 1;
     const int k0 = j * BN;
-    if (j + 1 < nt) {
-      load_gathered(kr, R.k, R.kp, R, b, h, bh, n, k0 + BN + 4 * rq, dc);
-      load_gathered(vr, R.v, R.vp, R, b, h, bh, n, k0 + BN + 4 * rq, dc);
-    }
-    if (k0 <= qw + 31) {
-      floatx16 s[2] = {floatx16{}, floatx16{}};
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) s[kb] = mfma(ld_row(Ks[cur], kb * 32 + l32, 16 * c + 8 * hh), qf[c], s[kb]);
-      }
-      const bool diag = (k0 + BN - 1 > qw) || (k0 + BN > n);
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          float x = s[kb][v] * a.sl2;
-          if (diag) {
-            const int key = k0 + kb * 32 + 8 * (v >> 2) + 4 * hh + (v & 3);
-            if (key > my_q || key >= n) x = -INFINITY;
-          }
-          s[kb][v] = x;
-          mx = fmaxf(mx, x);
-        }
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_i, mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = ex2(m_i - m_use);
-      float ls = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float pv = ex2(s[kb][v] - m_use);
-          s[kb][v] = pv;
-          ls += pv;
-        }
-      }
-      ls += __shfl_xor(ls, 32);
-      l_i = l_i * alpha + ls;
-      m_i = m_new;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) o[d] *= alpha;
-      u32x4 pf[2][2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        pf[kb][0] = pack_frag(s[kb], 0);
-        pf[kb][1] = pack_frag(s[kb], 1);
-      }
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int c2 = 0; c2 < 2; ++c2) o[d] = mfma(ld_tr(Vt[cur], d * 32 + l32, kb * 32 + 16 * c2, hh), pf[kb][c2], o[d]);
-        }
-      }
-    }
-    if (j + 1 < nt) {
-      store_rowmajor(kr, Ks[cur ^ 1], rq, dc);
-      store_transposed(vr, Vt[cur ^ 1], rq, dc);
-    }
+    const bf16_t* Ks = lds + cur * TILE;
+    const bf16_t* Vs = lds + (2 + cur) * TILE;
+    if (j + 1 < nt)
+      issue_gathered(lds + (cur ^ 1) * TILE, m.k, m.kp, lds + (2 + (cur ^ 1)) * TILE, m.v, m.vp, m, k0 + BN, wave,
+                     lane);
+    if (k0 <= qw + 31) fwd_tile(st, qf, Ks, Vs, k0, my_q, n, lane, a.sl2, j >= nfull);
+    wait_loads();
     __syncthreads();
   }
 
   if (my_q >= n) return;
-  const float inv_l = l_i > 0.f ? 1.0f / l_i : 0.f;
+  const float l = st.l + __shfl_xor(st.l, 32);
+  const float inv_l = l > 0.f ? 1.0f / l : 0.f;
   if (EPI == 0) {
-    bf16_t* orow = a.out + ((int64_t)bh * n + my_q) * LH_D;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        u32x2 w;
-        w.x = cvt2(o[d][4 * g + 0] * inv_l, o[d][4 * g + 1] * inv_l);
-        w.y = cvt2(o[d][4 * g + 2] * inv_l, o[d][4 * g + 3] * inv_l);
-        *reinterpret_cast<u32x2*>(orow + d * 32 + 8 * g + 4 * hh) = w;
-      }
-    }
-    if (hh == 0) a.lse[(int64_t)bh * n + my_q] = l_i > 0.f ? m_i + __log2f(l_i) : -INFINITY;
+    store_rows_bf16(a.out + ((int64_t)bh * n + my_q) * LH_D, st.o, inv_l, hh);
+    if (hh == 0) a.lse[(int64_t)bh * n + my_q] = l > 0.f ? st.m * a.sl2 + __log2f(l) : -INFINITY;
   } else {
     float ss = 0.f;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
 #pragma unroll
       for (int v = 0; v < 16; v += 2) {
-        const uint32_t w = cvt2(o[d][v] * inv_l, o[d][v + 1] * inv_l);
+        const uint32_t w = cvt2(st.o[d][v] * inv_l, st.o[d][v + 1] * inv_l);
         const float x0 = __uint_as_float(w << 16), x1 = __uint_as_float(w & 0xffff0000u);
         ss = fmaf(x0, x0, ss);
         ss = fmaf(x1, x1, ss);
@@ -303,7 +360,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
     }
     ss += __shfl_xor(ss, 32);
     if (hh == 0) {
-      const int vh = h;  // virtual head
+      const int vh = bh % a.H;  // virtual head of the dilated view
+      const int b = bh / a.H;
       const int t = my_q * a.dil + vh / a.Ho;
       const int ho = vh % a.Ho;
       a.scores[((int64_t)b * a.Ho + ho) * a.S_tot + t] = __uint_as_float(cvt2(sqrtf(ss), 0.f) << 16);
@@ -314,267 +372,218 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
 // ===========================================================================
 // backward dQ (query-stationary)
 // ===========================================================================
+__device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], const u32x4 (&qf)[8], const u32x4 (&df)[8],
+                                        const bf16_t* Ks, const bf16_t* Vs, int k0, int my_q, int n, int lane,
+                                        float sl2, float nlse, float dlt, bool mask) {
+  const int l32 = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    floatx16 s = mfma(op_row(Ks, kb * 32 + l32, 0, hh), qf[0], floatx16{});
+    floatx16 dp = mfma(op_row(Vs, kb * 32 + l32, 0, hh), df[0], floatx16{});
+#pragma unroll
+    for (int c = 1; c < 8; ++c) {
+      s = mfma(op_row(Ks, kb * 32 + l32, c, hh), qf[c], s);
+      dp = mfma(op_row(Vs, kb * 32 + l32, c, hh), df[c], dp);
+    }
+    if (mask) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = k0 + kb * 32 + slot_key(v, hh);
+        if (key > my_q || key >= n) s[v] = -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s[v] = ex2(fmaf(s[v], sl2, nlse)) * (dp[v] - dlt);
+    const u32x4 f0 = pack_frag(s, 0), f1 = pack_frag(s, 1);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      acc[d] = mfma(op_tr(Ks, kb * 32, d, lane), f0, acc[d]);
+      acc[d] = mfma(op_tr(Ks, kb * 32 + 16, d, lane), f1, acc[d]);
+    }
+  }
+}
+
 __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(const AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16_t Ks[2][BN * RS];
-  __shared__ __attribute__((aligned(16))) bf16_t Vs[2][BN * RS];
-  __shared__ __attribute__((aligned(16))) bf16_t Kt[2][LH_D * TS];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  __shared__ __attribute__((aligned(1024))) bf16_t lds[4 * TILE];  // K0 K1 V0 V1
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int bh, qb;
   schedule(blockIdx.x, a.nq, a.BH, bh, qb, true);
-  const int b = bh / a.H, h = bh % a.H, n = a.n;
-  const Rows& R = a.R;
+  const int n = a.n;
+  const BhRows m = bh_rows(a, bh);
   const int q0 = qb * BM, qw = q0 + wave * 32, my_q = qw + l32;
+  const int qc = min(my_q, n - 1);
 
   u32x4 qf[8], df[8];
-  float lse2 = 0.f, dlt = 0.f;
-  if (my_q < n) {
+  {
     bool pooled;
-    const int64_t o = row_off(R, b, h, bh, n, my_q, pooled);
-    const bf16_t* p = (pooled ? R.qp : R.q) + o + 8 * hh;
-    const bf16_t* pd = a.dout + ((int64_t)bh * n + my_q) * LH_D + 8 * hh;
+    const uint32_t o = row_off(m, my_q, pooled) + 8 * hh;
+    const bf16_t* p = (pooled ? m.qp : m.q) + o;
+    const bf16_t* pd = a.dout + ((int64_t)bh * n + qc) * LH_D + 8 * hh;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      qf[c] = *reinterpret_cast<const u32x4*>(p + 16 * c);
-      df[c] = *reinterpret_cast<const u32x4*>(pd + 16 * c);
+      qf[c] = ldg16(p + 16 * c);
+      df[c] = ldg16(pd + 16 * c);
     }
-    lse2 = a.lse_in[(int64_t)bh * n + my_q];
-    dlt = a.delta[(int64_t)bh * n + my_q];
-  } else {
-#pragma unroll
-    for (int c = 0; c < 8; ++c) { qf[c] = u32x4{0u, 0u, 0u, 0u}; df[c] = u32x4{0u, 0u, 0u, 0u}; }
   }
+  const float nlse = -a.lse_in[(int64_t)bh * n + qc];
+  const float dlt = a.delta[(int64_t)bh * n + qc];
 
   const int kend = min(q0 + BM, n);
   const int nt = (kend + BN - 1) / BN;
-  const int rq = tid & 15, dc = tid >> 4;
-  Tile4 kr, vr;
-  load_gathered(kr, R.k, R.kp, R, b, h, bh, n, 4 * rq, dc);
-  load_gathered(vr, R.v, R.vp, R, b, h, bh, n, 4 * rq, dc);
-  store_rowmajor(kr, Ks[0], rq, dc);
-  store_transposed(kr, Kt[0], rq, dc);
-  store_rowmajor(vr, Vs[0], rq, dc);
+  issue_gathered(lds, m.k, m.kp, lds + 2 * TILE, m.v, m.vp, m, 0, wave, lane);
+  wait_loads();
   __syncthreads();
 
   floatx16 acc[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) acc[d] = floatx16{};
+  const int nfull = min((qw + 1) / BN, n / BN);
 
   for (int j = 0; j < nt; ++j) {
     const int cur = j & 1;
     const int k0 = j * BN;
-    if (j + 1 < nt) {
-      load_gathered(kr, R.k, R.kp, R, b, h, bh, n, k0 + BN + 4 * rq, dc);
-      load_gathered(vr, R.v, R.vp, R, b, h, bh, n, k0 + BN + 4 * rq, dc);
-    }
-    if (k0 <= qw + 31) {
-      floatx16 s[2] = {floatx16{}, floatx16{}}, dp[2] = {floatx16{}, floatx16{}};
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          s[kb] = mfma(ld_row(Ks[cur], kb * 32 + l32, 16 * c + 8 * hh), qf[c], s[kb]);
-          dp[kb] = mfma(ld_row(Vs[cur], kb * 32 + l32, 16 * c + 8 * hh), df[c], dp[kb]);
-        }
-      }
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int key = k0 + kb * 32 + 8 * (v >> 2) + 4 * hh + (v & 3);
-          const bool masked = key > my_q || key >= n || my_q >= n;
-          const float p = masked ? 0.f : ex2(s[kb][v] * a.sl2 - lse2);
-          s[kb][v] = p * (dp[kb][v] - dlt);
-        }
-      }
-      u32x4 sf[2][2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        sf[kb][0] = pack_frag(s[kb], 0);
-        sf[kb][1] = pack_frag(s[kb], 1);
-      }
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int c2 = 0; c2 < 2; ++c2)
-            acc[d] = mfma(ld_tr(Kt[cur], d * 32 + l32, kb * 32 + 16 * c2, hh), sf[kb][c2], acc[d]);
-        }
-      }
-    }
-    if (j + 1 < nt) {
-      store_rowmajor(kr, Ks[cur ^ 1], rq, dc);
-      store_transposed(kr, Kt[cur ^ 1], rq, dc);
-      store_rowmajor(vr, Vs[cur ^ 1], rq, dc);
-    }
+    const bf16_t* Ks = lds + cur * TILE;
+    const bf16_t* Vs = lds + (2 + cur) * TILE;
+    if (j + 1 < nt)
+      issue_gathered(lds + (cur ^ 1) * TILE, m.k, m.kp, lds + (2 + (cur ^ 1)) * TILE, m.v, m.vp, m, k0 + BN, wave,
+                     lane);
+    if (k0 <= qw + 31) dq_tile(acc, qf, df, Ks, Vs, k0, my_q, n, lane, a.sl2, nlse, dlt, j >= nfull);
+    wait_loads();
     __syncthreads();
   }
 
   if (my_q >= n) return;
-  bf16_t* orow = a.dq + ((int64_t)bh * n + my_q) * LH_D;
-  const float sc = a.scale;
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      u32x2 w;
-      w.x = cvt2(acc[d][4 * g + 0] * sc, acc[d][4 * g + 1] * sc);
-      w.y = cvt2(acc[d][4 * g + 2] * sc, acc[d][4 * g + 3] * sc);
-      *reinterpret_cast<u32x2*>(orow + d * 32 + 8 * g + 4 * hh) = w;
-    }
-  }
+  store_rows_bf16(a.dq + ((int64_t)bh * n + my_q) * LH_D, acc, a.scale, hh);
 }
 
 // ===========================================================================
 // backward dK, dV (key-stationary)
 // ===========================================================================
+__device__ __forceinline__ void dkdv_tile(floatx16 (&dka)[4], floatx16 (&dva)[4], const u32x4 (&kf)[8],
+                                          const u32x4 (&vf)[8], const bf16_t* Qs, const bf16_t* Ds, const float* Ls,
+                                          const float* Dl, int q0t, int my_k, int n, int lane, float sl2, bool mask) {
+  const int l32 = lane & 31, hh = lane >> 5;
+  // one 32-query half at a time keeps the live set to one S and one dP block
+#pragma unroll 1
+  for (int qb = 0; qb < 2; ++qb) {
+    floatx16 s = mfma(op_row(Qs, qb * 32 + l32, 0, hh), kf[0], floatx16{});
+    floatx16 dp = mfma(op_row(Ds, qb * 32 + l32, 0, hh), vf[0], floatx16{});
+#pragma unroll
+    for (int c = 1; c < 8; ++c) {
+      s = mfma(op_row(Qs, qb * 32 + l32, c, hh), kf[c], s);
+      dp = mfma(op_row(Ds, qb * 32 + l32, c, hh), vf[c], dp);
+    }
+    if (mask) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int q = q0t + qb * 32 + slot_key(v, hh);
+        if (my_k > q || q >= n) s[v] = -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int qi = qb * 32 + 8 * g + 4 * hh;
+      const float4 l4 = *reinterpret_cast<const float4*>(Ls + qi);  // holds -lse
+      const float4 d4 = *reinterpret_cast<const float4*>(Dl + qi);
+      const float nl[4] = {l4.x, l4.y, l4.z, l4.w};
+      const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int v = 4 * g + e;
+        const float p = ex2(fmaf(s[v], sl2, nl[e]));
+        s[v] = p;
+        dp[v] = p * (dp[v] - dd[e]);
+      }
+    }
+    const u32x4 p0 = pack_frag(s, 0), p1 = pack_frag(s, 1);
+    const u32x4 s0 = pack_frag(dp, 0), s1 = pack_frag(dp, 1);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      dva[d] = mfma(op_tr(Ds, qb * 32, d, lane), p0, dva[d]);
+      dva[d] = mfma(op_tr(Ds, qb * 32 + 16, d, lane), p1, dva[d]);
+      dka[d] = mfma(op_tr(Qs, qb * 32, d, lane), s0, dka[d]);
+      dka[d] = mfma(op_tr(Qs, qb * 32 + 16, d, lane), s1, dka[d]);
+    }
+  }
+}
+
 __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16_t Qs[2][BN * RS];
-  __shared__ __attribute__((aligned(16))) bf16_t Ds[2][BN * RS];
-  __shared__ __attribute__((aligned(16))) bf16_t Qt[2][LH_D * TS];
-  __shared__ __attribute__((aligned(16))) bf16_t Dt[2][LH_D * TS];
+  __shared__ __attribute__((aligned(1024))) bf16_t lds[4 * TILE];  // Q0 Q1 dO0 dO1
   __shared__ __attribute__((aligned(16))) float Ls[2][BN];
   __shared__ __attribute__((aligned(16))) float Dl[2][BN];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int bh, kblk;
   schedule(blockIdx.x, a.nq, a.BH, bh, kblk, false);  // early key blocks see the most queries
-  const int b = bh / a.H, h = bh % a.H, n = a.n;
-  const Rows& R = a.R;
+  const int n = a.n;
+  const BhRows m = bh_rows(a, bh);
   const int k0 = kblk * BM, kw = k0 + wave * 32, my_k = kw + l32;
 
   u32x4 kf[8], vf[8];
-  if (my_k < n) {
+  {
     bool pooled;
-    const int64_t o = row_off(R, b, h, bh, n, my_k, pooled);
-    const bf16_t* pk = (pooled ? R.kp : R.k) + o + 8 * hh;
-    const bf16_t* pv = (pooled ? R.vp : R.v) + o + 8 * hh;
+    const uint32_t o = row_off(m, my_k, pooled) + 8 * hh;
+    const bf16_t* pk = (pooled ? m.kp : m.k) + o;
+    const bf16_t* pv = (pooled ? m.vp : m.v) + o;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      kf[c] = *reinterpret_cast<const u32x4*>(pk + 16 * c);
-      vf[c] = *reinterpret_cast<const u32x4*>(pv + 16 * c);
+      kf[c] = ldg16(pk + 16 * c);
+      vf[c] = ldg16(pv + 16 * c);
     }
-  } else {
-#pragma unroll
-    for (int c = 0; c < 8; ++c) { kf[c] = u32x4{0u, 0u, 0u, 0u}; vf[c] = u32x4{0u, 0u, 0u, 0u}; }
   }
 
   const int jt0 = k0 / BN;
   const int nt = (n + BN - 1) / BN;
-  const int rq = tid & 15, dc = tid >> 4;
   const bf16_t* dbase = a.dout + (int64_t)bh * n * LH_D;
   const float* lrow = a.lse_in + (int64_t)bh * n;
   const float* drow = a.delta + (int64_t)bh * n;
-  Tile4 qr, dr;
   float lv = 0.f;
   {
     const int q0t = jt0 * BN;
-    load_gathered(qr, R.q, R.qp, R, b, h, bh, n, q0t + 4 * rq, dc);
-    load_dense(dr, dbase, n, q0t + 4 * rq, dc);
+    issue_gathered(lds, m.q, m.qp, nullptr, nullptr, nullptr, m, q0t, wave, lane);
+    issue_dense(lds + 2 * TILE, dbase, n - 1, q0t, wave, lane);
     if (tid < 2 * BN) {
-      const int qq = q0t + (tid & (BN - 1));
-      lv = qq < n ? (tid < BN ? lrow[qq] : drow[qq]) : 0.f;
+      const int qq = min(q0t + (tid & (BN - 1)), n - 1);
+      lv = tid < BN ? -lrow[qq] : drow[qq];
     }
-    store_rowmajor(qr, Qs[0], rq, dc);
-    store_transposed(qr, Qt[0], rq, dc);
-    store_rowmajor(dr, Ds[0], rq, dc);
-    store_transposed(dr, Dt[0], rq, dc);
     if (tid < BN) Ls[0][tid] = lv; else if (tid < 2 * BN) Dl[0][tid - BN] = lv;
   }
+  wait_loads();
   __syncthreads();
 
   floatx16 dka[4], dva[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) { dka[d] = floatx16{}; dva[d] = floatx16{}; }
+  // query tiles whose 64 queries are all >= this wave's last key and < n need no mask
+  const int jfull = (kw + 31 + BN - 1) / BN;
 
   for (int j = jt0; j < nt; ++j) {
     const int cur = (j - jt0) & 1;
     const int q0t = j * BN;
+    const bf16_t* Qs = lds + cur * TILE;
+    const bf16_t* Ds = lds + (2 + cur) * TILE;
     if (j + 1 < nt) {
       const int qn = q0t + BN;
-      load_gathered(qr, R.q, R.qp, R, b, h, bh, n, qn + 4 * rq, dc);
-      load_dense(dr, dbase, n, qn + 4 * rq, dc);
+      issue_gathered(lds + (cur ^ 1) * TILE, m.q, m.qp, nullptr, nullptr, nullptr, m, qn, wave, lane);
+      issue_dense(lds + (2 + (cur ^ 1)) * TILE, dbase, n - 1, qn, wave, lane);
       if (tid < 2 * BN) {
-        const int qq = qn + (tid & (BN - 1));
-        lv = qq < n ? (tid < BN ? lrow[qq] : drow[qq]) : 0.f;
+        const int qq = min(qn + (tid & (BN - 1)), n - 1);
+        lv = tid < BN ? -lrow[qq] : drow[qq];
       }
     }
-    if (q0t + BN - 1 >= kw) {
-      floatx16 s[2] = {floatx16{}, floatx16{}}, dp[2] = {floatx16{}, floatx16{}};
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          s[qb] = mfma(ld_row(Qs[cur], qb * 32 + l32, 16 * c + 8 * hh), kf[c], s[qb]);
-          dp[qb] = mfma(ld_row(Ds[cur], qb * 32 + l32, 16 * c + 8 * hh), vf[c], dp[qb]);
-        }
-      }
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int qi = qb * 32 + 8 * g + 4 * hh;
-          const float4 l4 = *reinterpret_cast<const float4*>(&Ls[cur][qi]);
-          const float4 d4 = *reinterpret_cast<const float4*>(&Dl[cur][qi]);
-          const float lq[4] = {l4.x, l4.y, l4.z, l4.w};
-          const float dq4[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int v = 4 * g + e;
-            const int q = q0t + qi + e;
-            const bool masked = my_k > q || q >= n || my_k >= n;
-            const float p = masked ? 0.f : ex2(s[qb][v] * a.sl2 - lq[e]);
-            s[qb][v] = p;
-            dp[qb][v] = p * (dp[qb][v] - dq4[e]);
-          }
-        }
-      }
-      u32x4 pf[2][2], sf[2][2];
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        pf[qb][0] = pack_frag(s[qb], 0);
-        pf[qb][1] = pack_frag(s[qb], 1);
-        sf[qb][0] = pack_frag(dp[qb], 0);
-        sf[qb][1] = pack_frag(dp[qb], 1);
-      }
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-#pragma unroll
-          for (int c2 = 0; c2 < 2; ++c2) {
-            dva[d] = mfma(ld_tr(Dt[cur], d * 32 + l32, qb * 32 + 16 * c2, hh), pf[qb][c2], dva[d]);
-            dka[d] = mfma(ld_tr(Qt[cur], d * 32 + l32, qb * 32 + 16 * c2, hh), sf[qb][c2], dka[d]);
-          }
-        }
-      }
-    }
+    if (q0t + BN - 1 >= kw)
+      dkdv_tile(dka, dva, kf, vf, Qs, Ds, Ls[cur], Dl[cur], q0t, my_k, n, lane, a.sl2, !(j >= jfull && q0t + BN <= n));
     if (j + 1 < nt) {
-      store_rowmajor(qr, Qs[cur ^ 1], rq, dc);
-      store_transposed(qr, Qt[cur ^ 1], rq, dc);
-      store_rowmajor(dr, Ds[cur ^ 1], rq, dc);
-      store_transposed(dr, Dt[cur ^ 1], rq, dc);
       if (tid < BN) Ls[cur ^ 1][tid] = lv; else if (tid < 2 * BN) Dl[cur ^ 1][tid - BN] = lv;
     }
+    wait_loads();
     __syncthreads();
   }
 
   if (my_k >= n) return;
-  bf16_t* krow = a.dk + ((int64_t)bh * n + my_k) * LH_D;
-  bf16_t* vrow = a.dv + ((int64_t)bh * n + my_k) * LH_D;
-  const float sc = a.scale;
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      u32x2 w;
-      w.x = cvt2(dka[d][4 * g + 0] * sc, dka[d][4 * g + 1] * sc);
-      w.y = cvt2(dka[d][4 * g + 2] * sc, dka[d][4 * g + 3] * sc);
-      *reinterpret_cast<u32x2*>(krow + d * 32 + 8 * g + 4 * hh) = w;
-      w.x = cvt2(dva[d][4 * g + 0], dva[d][4 * g + 1]);
-      w.y = cvt2(dva[d][4 * g + 2], dva[d][4 * g + 3]);
-      *reinterpret_cast<u32x2*>(vrow + d * 32 + 8 * g + 4 * hh) = w;
-    }
-  }
+  store_rows_bf16(a.dk + ((int64_t)bh * n + my_k) * LH_D, dka, a.scale, hh);
+  store_rows_bf16(a.dv + ((int64_t)bh * n + my_k) * LH_D, dva, 1.0f, hh);
 }
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -584,14 +593,19 @@ int fill_rows(AttnArgs& a, const void* q, const void* k, const void* v, int64_t 
               const int32_t* indices, int B, int H, int n, int D, float scale) {
   if (D != LH_D) return LH_ERR_UNSUPPORTED;
   if (!q || !k || !v || B <= 0 || H <= 0 || n <= 0) return LH_ERR_INVALID_ARG;
-  if (!al16(q) || !al16(k) || !al16(v) || (sb | ss | sh) % 8) return LH_ERR_INVALID_ARG;
+  if (!al16(q) || !al16(k) || !al16(v) || (sb | ss | sh) % 8 || ss <= 0) return LH_ERR_INVALID_ARG;
   const bool need_pool = indices != nullptr;  // pooled rows only reachable through an index map
-  if (need_pool && (!qp || !kp || !vp || !al16(qp) || !al16(kp) || !al16(vp) || (pb | ps | ph) % 8))
+  if (need_pool && (!qp || !kp || !vp || !al16(qp) || !al16(kp) || !al16(vp) || (pb | ps | ph) % 8 || ps <= 0))
     return LH_ERR_INVALID_ARG;
   if (!(scale > 0.f)) return LH_ERR_INVALID_ARG;
+  // Row offsets inside one (b, h) are 32-bit.  Base rows are < split (or < n
+  // without an index map); pooled rows r - split are < split too, as every
+  // pyramid's pooled levels are shorter than its base level.
+  const long long rows = need_pool ? split : n;
+  if (rows * ss + LH_D > 0x7fffffffLL || (need_pool && rows * ps + LH_D > 0x7fffffffLL)) return LH_ERR_UNSUPPORTED;
   a.R.q = (const bf16_t*)q; a.R.k = (const bf16_t*)k; a.R.v = (const bf16_t*)v;
   a.R.qp = (const bf16_t*)(qp ? qp : q); a.R.kp = (const bf16_t*)(kp ? kp : k); a.R.vp = (const bf16_t*)(vp ? vp : v);
-  a.R.sb = sb; a.R.ss = ss; a.R.sh = sh; a.R.pb = pb; a.R.ps = ps; a.R.ph = ph;
+  a.R.sb = sb; a.R.ss = ss; a.R.sh = sh; a.R.pb = pb; a.R.ps = need_pool ? ps : ss; a.R.ph = ph;
   a.R.split = indices ? split : 0x7fffffff;
   a.R.idx = indices;
   a.B = B; a.H = H; a.n = n; a.BH = B * H;
