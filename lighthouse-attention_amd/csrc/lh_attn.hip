@@ -150,17 +150,28 @@ __device__ __forceinline__ void g2l16(const bf16_t* g, bf16_t* lds_base) {
   __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_base, 16, 0, 0);
 }
 
-// Wave w fills rows 16w .. 16w+15 of one tile (two tiles sharing the row map when
-// tile2 != null) from selected rows row0 .. row0+63: four 1 KB loads of 4 rows.
-__device__ __forceinline__ void issue_gathered(bf16_t* tile, const bf16_t* base, const bf16_t* pool, bf16_t* tile2,
-                                               const bf16_t* base2, const bf16_t* pool2, const BhRows& m, int row0,
-                                               int w, int lane) {
+// Wave w fills rows 16w .. 16w+15 of a 64-row tile with four 1 KB direct loads
+// of 4 rows each.  The selected-row indices of those rows are loaded one tile
+// ahead (load_rows) so issuing a tile never waits on an index load.
+__device__ __forceinline__ void load_rows(int (&r)[4], const BhRows& m, int row0, int w, int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int s = min(row0 + 16 * w + 4 * i + (lane >> 4), m.last);
+    r[i] = m.idx ? m.idx[s] : s;
+  }
+}
+
+// (tile2 != null: a second tensor with the same row map, e.g. V beside K)
+__device__ __forceinline__ void issue_rows(bf16_t* tile, const bf16_t* base, const bf16_t* pool, bf16_t* tile2,
+                                           const bf16_t* base2, const bf16_t* pool2, const BhRows& m,
+                                           const int (&rr)[4], int w, int lane) {
   const int rsub = lane >> 4, slot = lane & 15;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 16 * w + 4 * i + rsub;
-    bool pooled;
-    const uint32_t o = row_off(m, row0 + r, pooled) + 8 * (slot ^ swz(r));
+    const bool pooled = rr[i] >= m.split;
+    const uint32_t o = (pooled ? (uint32_t)(rr[i] - m.split) * (uint32_t)m.ps : (uint32_t)rr[i] * (uint32_t)m.ss) +
+                       8 * (slot ^ swz(r));
     g2l16((pooled ? pool : base) + o, tile + (16 * w + 4 * i) * LH_D);
     if (tile2) g2l16((pooled ? pool2 : base2) + o, tile2 + (16 * w + 4 * i) * LH_D);
   }
@@ -233,12 +244,14 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
                                          int k0, int my_q, int n, int lane, float sl2, bool mask) {
   const int l32 = lane & 31, hh = lane >> 5;
   floatx16 s[2];
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     s[kb] = mfma(op_row(Ks, kb * 32 + l32, 0, hh), qf[0], floatx16{});
 #pragma unroll
     for (int c = 1; c < 8; ++c) s[kb] = mfma(op_row(Ks, kb * 32 + l32, c, hh), qf[c], s[kb]);
   }
+  __builtin_amdgcn_s_setprio(0);
   if (mask) {  // wave-uniform: only tiles that cross the diagonal or the end
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -283,6 +296,7 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
     pf[kb][0] = pack_frag(s[kb], 0);
     pf[kb][1] = pack_frag(s[kb], 1);
   }
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
 #pragma unroll
@@ -291,11 +305,15 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
       for (int c2 = 0; c2 < 2; ++c2) st.o[d] = mfma(op_tr(Vs, kb * 32 + 16 * c2, d, lane), pf[kb][c2], st.o[d]);
     }
   }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 template <int EPI>  // 0: O + LSE;  1: bf16-rounded row norms of O into `scores`
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
-  __shared__ __attribute__((aligned(1024))) bf16_t lds[4 * TILE];  // K0 K1 V0 V1
+  __shared__ __attribute__((aligned(1024))) bf16_t K0[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t K1[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t V0[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t V1[TILE];
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int bh, qb;
@@ -315,7 +333,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
 
   const int kend = min(q0 + BM, n);
   const int nt = (kend + BN - 1) / BN;
-  issue_gathered(lds, m.k, m.kp, lds + 2 * TILE, m.v, m.vp, m, 0, wave, lane);
+  int rr[4];
+  load_rows(rr, m, 0, wave, lane);
+  issue_rows(K0, m.k, m.kp, V0, m.v, m.vp, m, rr, wave, lane);
+  load_rows(rr, m, BN, wave, lane);
   wait_loads();
   __syncthreads();
 
@@ -327,17 +348,17 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
   // tiles whose 64 keys are all <= this wave's first query and < n need no mask
   const int nfull = min((qw + 1) / BN, n / BN);
 
-  for (int j = 0; j < nt; ++j) {
-    const int cur = j & 1;
+  auto step = [&](int j, const bf16_t* Ks, const bf16_t* Vs, bf16_t* Kn, bf16_t* Vn) {
     const int k0 = j * BN;
-    const bf16_t* Ks = lds + cur * TILE;
-    const bf16_t* Vs = lds + (2 + cur) * TILE;
-    if (j + 1 < nt)
-      issue_gathered(lds + (cur ^ 1) * TILE, m.k, m.kp, lds + (2 + (cur ^ 1)) * TILE, m.v, m.vp, m, k0 + BN, wave,
-                     lane);
-    if (k0 <= qw + 31) fwd_tile(st, qf, Ks, Vs, k0, my_q, n, lane, a.sl2, j >= nfull);
+    if (j + 1 < nt) issue_rows(Kn, m.k, m.kp, Vn, m.v, m.vp, m, rr, wave, lane);
+    if (j + 2 < nt) load_rows(rr, m, k0 + 2 * BN, wave, lane);
+    if (j < nt && k0 <= qw + 31) fwd_tile(st, qf, Ks, Vs, k0, my_q, n, lane, a.sl2, j >= nfull);
     wait_loads();
     __syncthreads();
+  };
+  for (int j = 0; j < nt; j += 2) {
+    step(j, K0, V0, K1, V1);
+    step(j + 1, K1, V1, K0, V0);
   }
 
   if (my_q >= n) return;
@@ -378,6 +399,7 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], const u32x4 (&qf)[8]
   const int l32 = lane & 31, hh = lane >> 5;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
+    __builtin_amdgcn_s_setprio(1);
     floatx16 s = mfma(op_row(Ks, kb * 32 + l32, 0, hh), qf[0], floatx16{});
     floatx16 dp = mfma(op_row(Vs, kb * 32 + l32, 0, hh), df[0], floatx16{});
 #pragma unroll
@@ -385,6 +407,7 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], const u32x4 (&qf)[8]
       s = mfma(op_row(Ks, kb * 32 + l32, c, hh), qf[c], s);
       dp = mfma(op_row(Vs, kb * 32 + l32, c, hh), df[c], dp);
     }
+    __builtin_amdgcn_s_setprio(0);
     if (mask) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
@@ -395,16 +418,21 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], const u32x4 (&qf)[8]
 #pragma unroll
     for (int v = 0; v < 16; ++v) s[v] = ex2(fmaf(s[v], sl2, nlse)) * (dp[v] - dlt);
     const u32x4 f0 = pack_frag(s, 0), f1 = pack_frag(s, 1);
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       acc[d] = mfma(op_tr(Ks, kb * 32, d, lane), f0, acc[d]);
       acc[d] = mfma(op_tr(Ks, kb * 32 + 16, d, lane), f1, acc[d]);
     }
+    __builtin_amdgcn_s_setprio(0);
   }
 }
 
-__global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(const AttnArgs a) {
-  __shared__ __attribute__((aligned(1024))) bf16_t lds[4 * TILE];  // K0 K1 V0 V1
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnArgs a) {
+  __shared__ __attribute__((aligned(1024))) bf16_t K0[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t K1[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t V0[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t V1[TILE];
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int bh, qb;
@@ -431,7 +459,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(const AttnArgs a) {
 
   const int kend = min(q0 + BM, n);
   const int nt = (kend + BN - 1) / BN;
-  issue_gathered(lds, m.k, m.kp, lds + 2 * TILE, m.v, m.vp, m, 0, wave, lane);
+  int rr[4];
+  load_rows(rr, m, 0, wave, lane);
+  issue_rows(K0, m.k, m.kp, V0, m.v, m.vp, m, rr, wave, lane);
+  load_rows(rr, m, BN, wave, lane);
   wait_loads();
   __syncthreads();
 
@@ -440,17 +471,17 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(const AttnArgs a) {
   for (int d = 0; d < 4; ++d) acc[d] = floatx16{};
   const int nfull = min((qw + 1) / BN, n / BN);
 
-  for (int j = 0; j < nt; ++j) {
-    const int cur = j & 1;
+  auto step = [&](int j, const bf16_t* Ks, const bf16_t* Vs, bf16_t* Kn, bf16_t* Vn) {
     const int k0 = j * BN;
-    const bf16_t* Ks = lds + cur * TILE;
-    const bf16_t* Vs = lds + (2 + cur) * TILE;
-    if (j + 1 < nt)
-      issue_gathered(lds + (cur ^ 1) * TILE, m.k, m.kp, lds + (2 + (cur ^ 1)) * TILE, m.v, m.vp, m, k0 + BN, wave,
-                     lane);
-    if (k0 <= qw + 31) dq_tile(acc, qf, df, Ks, Vs, k0, my_q, n, lane, a.sl2, nlse, dlt, j >= nfull);
+    if (j + 1 < nt) issue_rows(Kn, m.k, m.kp, Vn, m.v, m.vp, m, rr, wave, lane);
+    if (j + 2 < nt) load_rows(rr, m, k0 + 2 * BN, wave, lane);
+    if (j < nt && k0 <= qw + 31) dq_tile(acc, qf, df, Ks, Vs, k0, my_q, n, lane, a.sl2, nlse, dlt, j >= nfull);
     wait_loads();
     __syncthreads();
+  };
+  for (int j = 0; j < nt; j += 2) {
+    step(j, K0, V0, K1, V1);
+    step(j + 1, K1, V1, K0, V0);
   }
 
   if (my_q >= n) return;
@@ -465,8 +496,9 @@ __device__ __forceinline__ void dkdv_tile(floatx16 (&dka)[4], floatx16 (&dva)[4]
                                           const float* Dl, int q0t, int my_k, int n, int lane, float sl2, bool mask) {
   const int l32 = lane & 31, hh = lane >> 5;
   // one 32-query half at a time keeps the live set to one S and one dP block
-#pragma unroll 1
+#pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
+    __builtin_amdgcn_s_setprio(1);
     floatx16 s = mfma(op_row(Qs, qb * 32 + l32, 0, hh), kf[0], floatx16{});
     floatx16 dp = mfma(op_row(Ds, qb * 32 + l32, 0, hh), vf[0], floatx16{});
 #pragma unroll
@@ -474,6 +506,7 @@ __device__ __forceinline__ void dkdv_tile(floatx16 (&dka)[4], floatx16 (&dva)[4]
       s = mfma(op_row(Qs, qb * 32 + l32, c, hh), kf[c], s);
       dp = mfma(op_row(Ds, qb * 32 + l32, c, hh), vf[c], dp);
     }
+    __builtin_amdgcn_s_setprio(0);
     if (mask) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
@@ -498,6 +531,7 @@ __device__ __forceinline__ void dkdv_tile(floatx16 (&dka)[4], floatx16 (&dva)[4]
     }
     const u32x4 p0 = pack_frag(s, 0), p1 = pack_frag(s, 1);
     const u32x4 s0 = pack_frag(dp, 0), s1 = pack_frag(dp, 1);
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       dva[d] = mfma(op_tr(Ds, qb * 32, d, lane), p0, dva[d]);
@@ -505,13 +539,17 @@ __device__ __forceinline__ void dkdv_tile(floatx16 (&dka)[4], floatx16 (&dva)[4]
       dka[d] = mfma(op_tr(Qs, qb * 32, d, lane), s0, dka[d]);
       dka[d] = mfma(op_tr(Qs, qb * 32 + 16, d, lane), s1, dka[d]);
     }
+    __builtin_amdgcn_s_setprio(0);
   }
 }
 
 __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const AttnArgs a) {
-  __shared__ __attribute__((aligned(1024))) bf16_t lds[4 * TILE];  // Q0 Q1 dO0 dO1
-  __shared__ __attribute__((aligned(16))) float Ls[2][BN];
-  __shared__ __attribute__((aligned(16))) float Dl[2][BN];
+  __shared__ __attribute__((aligned(1024))) bf16_t Q0[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t Q1[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t D0[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t D1[TILE];
+  __shared__ __attribute__((aligned(16))) float L0[2 * BN];  // -lse then delta
+  __shared__ __attribute__((aligned(16))) float L1[2 * BN];
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   int bh, kblk;
@@ -538,17 +576,18 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
   const bf16_t* dbase = a.dout + (int64_t)bh * n * LH_D;
   const float* lrow = a.lse_in + (int64_t)bh * n;
   const float* drow = a.delta + (int64_t)bh * n;
-  float lv = 0.f;
-  {
-    const int q0t = jt0 * BN;
-    issue_gathered(lds, m.q, m.qp, nullptr, nullptr, nullptr, m, q0t, wave, lane);
-    issue_dense(lds + 2 * TILE, dbase, n - 1, q0t, wave, lane);
-    if (tid < 2 * BN) {
-      const int qq = min(q0t + (tid & (BN - 1)), n - 1);
-      lv = tid < BN ? -lrow[qq] : drow[qq];
-    }
-    if (tid < BN) Ls[0][tid] = lv; else if (tid < 2 * BN) Dl[0][tid - BN] = lv;
-  }
+  // threads 0..63 carry -lse, 64..127 delta of the tile's 64 queries
+  auto load_ld = [&](int q0t) -> float {
+    if (tid >= 2 * BN) return 0.f;
+    const int qq = min(q0t + (tid & (BN - 1)), n - 1);
+    return tid < BN ? -lrow[qq] : drow[qq];
+  };
+  int rr[4];
+  load_rows(rr, m, jt0 * BN, wave, lane);
+  issue_rows(Q0, m.q, m.qp, nullptr, nullptr, nullptr, m, rr, wave, lane);
+  issue_dense(D0, dbase, n - 1, jt0 * BN, wave, lane);
+  if (tid < 2 * BN) L0[tid] = load_ld(jt0 * BN);
+  load_rows(rr, m, (jt0 + 1) * BN, wave, lane);
   wait_loads();
   __syncthreads();
 
@@ -558,27 +597,24 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
   // query tiles whose 64 queries are all >= this wave's last key and < n need no mask
   const int jfull = (kw + 31 + BN - 1) / BN;
 
-  for (int j = jt0; j < nt; ++j) {
-    const int cur = (j - jt0) & 1;
+  auto step = [&](int j, const bf16_t* Qs, const bf16_t* Ds, const float* Ls, bf16_t* Qn, bf16_t* Dn, float* Ln) {
     const int q0t = j * BN;
-    const bf16_t* Qs = lds + cur * TILE;
-    const bf16_t* Ds = lds + (2 + cur) * TILE;
+    float lv = 0.f;
     if (j + 1 < nt) {
-      const int qn = q0t + BN;
-      issue_gathered(lds + (cur ^ 1) * TILE, m.q, m.qp, nullptr, nullptr, nullptr, m, qn, wave, lane);
-      issue_dense(lds + (2 + (cur ^ 1)) * TILE, dbase, n - 1, qn, wave, lane);
-      if (tid < 2 * BN) {
-        const int qq = min(qn + (tid & (BN - 1)), n - 1);
-        lv = tid < BN ? -lrow[qq] : drow[qq];
-      }
+      issue_rows(Qn, m.q, m.qp, nullptr, nullptr, nullptr, m, rr, wave, lane);
+      issue_dense(Dn, dbase, n - 1, q0t + BN, wave, lane);
+      lv = load_ld(q0t + BN);
     }
-    if (q0t + BN - 1 >= kw)
-      dkdv_tile(dka, dva, kf, vf, Qs, Ds, Ls[cur], Dl[cur], q0t, my_k, n, lane, a.sl2, !(j >= jfull && q0t + BN <= n));
-    if (j + 1 < nt) {
-      if (tid < BN) Ls[cur ^ 1][tid] = lv; else if (tid < 2 * BN) Dl[cur ^ 1][tid - BN] = lv;
-    }
+    if (j + 2 < nt) load_rows(rr, m, q0t + 2 * BN, wave, lane);
+    if (j < nt && q0t + BN - 1 >= kw)
+      dkdv_tile(dka, dva, kf, vf, Qs, Ds, Ls, Ls + BN, q0t, my_k, n, lane, a.sl2, !(j >= jfull && q0t + BN <= n));
+    if (j + 1 < nt && tid < 2 * BN) Ln[tid] = lv;
     wait_loads();
     __syncthreads();
+  };
+  for (int j = jt0; j < nt; j += 2) {
+    step(j, Q0, D0, L0, Q1, D1, L1);
+    step(j + 1, Q1, D1, L1, Q0, D0, L0);
   }
 
   if (my_k >= n) return;
