@@ -5,7 +5,8 @@
 // identity row map and a norm epilogue, the two SDPA calls of
 // DilatedLighthouseScorer.forward (:642-653).
 //
-// Layout choices (one 64-lane wave computes 32 queries x 64 keys per step):
+// Layout choices (one 64-lane wave computes 32 queries x 64 keys per step;
+// 8 waves share each K/V tile in the query-stationary kernels):
 //   * Scores are formed transposed, S^T = K Q^T, so an MFMA output column is a
 //     query: lane l holds query l%32 and 16 keys per 32x32 block.  Row max and
 //     row sum of the online softmax are in-lane plus one exchange with lane
@@ -37,7 +38,8 @@
 
 namespace {
 
-constexpr int BM = 128;  // queries (or keys) per workgroup: 4 waves x 32
+constexpr int BMK = 128;  // keys per workgroup of the key-stationary kernel: 4 waves x 32
+constexpr int QW = 8;     // waves per workgroup of the query-stationary kernels (32 queries each)
 constexpr int BN = 64;   // rows per LDS tile
 constexpr float RESCALE_LOG2 = 8.0f;
 
@@ -153,36 +155,39 @@ __device__ __forceinline__ void g2l16(const bf16_t* g, bf16_t* lds_base) {
 // Wave w fills rows 16w .. 16w+15 of a 64-row tile with four 1 KB direct loads
 // of 4 rows each.  The selected-row indices of those rows are loaded one tile
 // ahead (load_rows) so issuing a tile never waits on an index load.
-__device__ __forceinline__ void load_rows(int (&r)[4], const BhRows& m, int row0, int w, int lane) {
+template <int NW>
+__device__ __forceinline__ void load_rows(int (&r)[16 / NW], const BhRows& m, int row0, int w, int lane) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int s = min(row0 + 16 * w + 4 * i + (lane >> 4), m.last);
+  for (int i = 0; i < 16 / NW; ++i) {
+    const int s = min(row0 + (64 / NW) * w + 4 * i + (lane >> 4), m.last);
     r[i] = m.idx ? m.idx[s] : s;
   }
 }
 
 // (tile2 != null: a second tensor with the same row map, e.g. V beside K)
+template <int NW>
 __device__ __forceinline__ void issue_rows(bf16_t* tile, const bf16_t* base, const bf16_t* pool, bf16_t* tile2,
                                            const bf16_t* base2, const bf16_t* pool2, const BhRows& m,
-                                           const int (&rr)[4], int w, int lane) {
+                                           const int (&rr)[16 / NW], int w, int lane) {
   const int rsub = lane >> 4, slot = lane & 15;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 16 * w + 4 * i + rsub;
+  for (int i = 0; i < 16 / NW; ++i) {
+    const int r = (64 / NW) * w + 4 * i + rsub;
     const bool pooled = rr[i] >= m.split;
     const uint32_t o = (pooled ? (uint32_t)(rr[i] - m.split) * (uint32_t)m.ps : (uint32_t)rr[i] * (uint32_t)m.ss) +
                        8 * (slot ^ swz(r));
-    g2l16((pooled ? pool : base) + o, tile + (16 * w + 4 * i) * LH_D);
-    if (tile2) g2l16((pooled ? pool2 : base2) + o, tile2 + (16 * w + 4 * i) * LH_D);
+    g2l16((pooled ? pool : base) + o, tile + ((64 / NW) * w + 4 * i) * LH_D);
+    if (tile2) g2l16((pooled ? pool2 : base2) + o, tile2 + ((64 / NW) * w + 4 * i) * LH_D);
   }
 }
 
+template <int NW>
 __device__ __forceinline__ void issue_dense(bf16_t* tile, const bf16_t* base, int last, int row0, int w, int lane) {
   const int rsub = lane >> 4, slot = lane & 15;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 16 * w + 4 * i + rsub;
-    g2l16(base + (uint32_t)min(row0 + r, last) * LH_D + 8 * (slot ^ swz(r)), tile + (16 * w + 4 * i) * LH_D);
+  for (int i = 0; i < 16 / NW; ++i) {
+    const int r = (64 / NW) * w + 4 * i + rsub;
+    g2l16(base + (uint32_t)min(row0 + r, last) * LH_D + 8 * (slot ^ swz(r)), tile + ((64 / NW) * w + 4 * i) * LH_D);
   }
 }
 
@@ -309,7 +314,8 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
 }
 
 template <int EPI>  // 0: O + LSE;  1: bf16-rounded row norms of O into `scores`
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArgs a) {
+  constexpr int BM = 32 * QW;
   __shared__ __attribute__((aligned(1024))) bf16_t K0[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t K1[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t V0[TILE];
@@ -333,10 +339,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
 
   const int kend = min(q0 + BM, n);
   const int nt = (kend + BN - 1) / BN;
-  int rr[4];
-  load_rows(rr, m, 0, wave, lane);
-  issue_rows(K0, m.k, m.kp, V0, m.v, m.vp, m, rr, wave, lane);
-  load_rows(rr, m, BN, wave, lane);
+  int rr[16 / QW];
+  load_rows<QW>(rr, m, 0, wave, lane);
+  issue_rows<QW>(K0, m.k, m.kp, V0, m.v, m.vp, m, rr, wave, lane);
+  load_rows<QW>(rr, m, BN, wave, lane);
   wait_loads();
   __syncthreads();
 
@@ -350,8 +356,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const AttnArgs a) {
 
   auto step = [&](int j, const bf16_t* Ks, const bf16_t* Vs, bf16_t* Kn, bf16_t* Vn) {
     const int k0 = j * BN;
-    if (j + 1 < nt) issue_rows(Kn, m.k, m.kp, Vn, m.v, m.vp, m, rr, wave, lane);
-    if (j + 2 < nt) load_rows(rr, m, k0 + 2 * BN, wave, lane);
+    if (j + 1 < nt) issue_rows<QW>(Kn, m.k, m.kp, Vn, m.v, m.vp, m, rr, wave, lane);
+    if (j + 2 < nt) load_rows<QW>(rr, m, k0 + 2 * BN, wave, lane);
     if (j < nt && k0 <= qw + 31) fwd_tile(st, qf, Ks, Vs, k0, my_q, n, lane, a.sl2, j >= nfull);
     wait_loads();
     __syncthreads();
@@ -428,7 +434,8 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], const u32x4 (&qf)[8]
   }
 }
 
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const AttnArgs a) {
+  constexpr int BM = 32 * QW;
   __shared__ __attribute__((aligned(1024))) bf16_t K0[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t K1[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t V0[TILE];
@@ -459,10 +466,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnArgs a) {
 
   const int kend = min(q0 + BM, n);
   const int nt = (kend + BN - 1) / BN;
-  int rr[4];
-  load_rows(rr, m, 0, wave, lane);
-  issue_rows(K0, m.k, m.kp, V0, m.v, m.vp, m, rr, wave, lane);
-  load_rows(rr, m, BN, wave, lane);
+  int rr[16 / QW];
+  load_rows<QW>(rr, m, 0, wave, lane);
+  issue_rows<QW>(K0, m.k, m.kp, V0, m.v, m.vp, m, rr, wave, lane);
+  load_rows<QW>(rr, m, BN, wave, lane);
   wait_loads();
   __syncthreads();
 
@@ -473,8 +480,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const AttnArgs a) {
 
   auto step = [&](int j, const bf16_t* Ks, const bf16_t* Vs, bf16_t* Kn, bf16_t* Vn) {
     const int k0 = j * BN;
-    if (j + 1 < nt) issue_rows(Kn, m.k, m.kp, Vn, m.v, m.vp, m, rr, wave, lane);
-    if (j + 2 < nt) load_rows(rr, m, k0 + 2 * BN, wave, lane);
+    if (j + 1 < nt) issue_rows<QW>(Kn, m.k, m.kp, Vn, m.v, m.vp, m, rr, wave, lane);
+    if (j + 2 < nt) load_rows<QW>(rr, m, k0 + 2 * BN, wave, lane);
     if (j < nt && k0 <= qw + 31) dq_tile(acc, qf, df, Ks, Vs, k0, my_q, n, lane, a.sl2, nlse, dlt, j >= nfull);
     wait_loads();
     __syncthreads();
@@ -556,7 +563,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
   schedule(blockIdx.x, a.nq, a.BH, bh, kblk, false);  // early key blocks see the most queries
   const int n = a.n;
   const BhRows m = bh_rows(a, bh);
-  const int k0 = kblk * BM, kw = k0 + wave * 32, my_k = kw + l32;
+  const int k0 = kblk * BMK, kw = k0 + wave * 32, my_k = kw + l32;
 
   u32x4 kf[8], vf[8];
   {
@@ -583,11 +590,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
     return tid < BN ? -lrow[qq] : drow[qq];
   };
   int rr[4];
-  load_rows(rr, m, jt0 * BN, wave, lane);
-  issue_rows(Q0, m.q, m.qp, nullptr, nullptr, nullptr, m, rr, wave, lane);
-  issue_dense(D0, dbase, n - 1, jt0 * BN, wave, lane);
+  load_rows<4>(rr, m, jt0 * BN, wave, lane);
+  issue_rows<4>(Q0, m.q, m.qp, nullptr, nullptr, nullptr, m, rr, wave, lane);
+  issue_dense<4>(D0, dbase, n - 1, jt0 * BN, wave, lane);
   if (tid < 2 * BN) L0[tid] = load_ld(jt0 * BN);
-  load_rows(rr, m, (jt0 + 1) * BN, wave, lane);
+  load_rows<4>(rr, m, (jt0 + 1) * BN, wave, lane);
   wait_loads();
   __syncthreads();
 
@@ -601,11 +608,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
     const int q0t = j * BN;
     float lv = 0.f;
     if (j + 1 < nt) {
-      issue_rows(Qn, m.q, m.qp, nullptr, nullptr, nullptr, m, rr, wave, lane);
-      issue_dense(Dn, dbase, n - 1, q0t + BN, wave, lane);
+      issue_rows<4>(Qn, m.q, m.qp, nullptr, nullptr, nullptr, m, rr, wave, lane);
+      issue_dense<4>(Dn, dbase, n - 1, q0t + BN, wave, lane);
       lv = load_ld(q0t + BN);
     }
-    if (j + 2 < nt) load_rows(rr, m, q0t + 2 * BN, wave, lane);
+    if (j + 2 < nt) load_rows<4>(rr, m, q0t + 2 * BN, wave, lane);
     if (j < nt && q0t + BN - 1 >= kw)
       dkdv_tile(dka, dva, kf, vf, Qs, Ds, Ls, Ls + BN, q0t, my_k, n, lane, a.sl2, !(j >= jfull && q0t + BN <= n));
     if (j + 1 < nt && tid < 2 * BN) Ln[tid] = lv;
@@ -645,10 +652,10 @@ int fill_rows(AttnArgs& a, const void* q, const void* k, const void* v, int64_t 
   a.R.split = indices ? split : 0x7fffffff;
   a.R.idx = indices;
   a.B = B; a.H = H; a.n = n; a.BH = B * H;
-  a.nq = (n + BM - 1) / BM;
+  a.nq = (n + 32 * QW - 1) / (32 * QW);  // query blocks (the key-stationary launch resets it)
   a.scale = scale;
   a.sl2 = (float)((double)scale * 1.4426950408889634);
-  if ((long long)a.nq * a.BH > 0x7fffffffLL) return LH_ERR_UNSUPPORTED;
+  if ((long long)((n + 127) / 128) * a.BH > 0x7fffffffLL) return LH_ERR_UNSUPPORTED;
   return LH_OK;
 }
 
@@ -663,7 +670,8 @@ extern "C" int lh_attn_fwd(const void* q, const void* k, const void* v, int64_t 
   if (rc) return rc;
   if (!out || !lse || !al16(out)) return LH_ERR_INVALID_ARG;
   a.out = (bf16_t*)out; a.lse = lse;
-  hipLaunchKernelGGL(attn_fwd_kernel<0>, dim3(a.nq * a.BH), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+  hipLaunchKernelGGL(attn_fwd_kernel<0>, dim3(a.nq * a.BH), dim3(64 * QW), 0, reinterpret_cast<hipStream_t>(stream),
+                     a);
   LH_CHECK_LAUNCH();
   return LH_OK;
 }
@@ -684,11 +692,13 @@ int attn_bwd_parts(int parts, const void* q, const void* k, const void* v, int64
   a.dq = (bf16_t*)dq; a.dk = (bf16_t*)dk; a.dv = (bf16_t*)dv;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (parts & 1) {
-    hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(a.nq * a.BH), dim3(256), 0, st, a);
+    AttnArgs ak = a;
+    ak.nq = (a.n + BMK - 1) / BMK;
+    hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(ak.nq * ak.BH), dim3(256), 0, st, ak);
     LH_CHECK_LAUNCH();
   }
   if (parts & 2) {
-    hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3(a.nq * a.BH), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3(a.nq * a.BH), dim3(64 * QW), 0, st, a);
     LH_CHECK_LAUNCH();
   }
   return LH_OK;
@@ -739,7 +749,7 @@ extern "C" int lh_dilated_scores(const void* xq, const void* xk, const void* xv,
     if (rc) return rc;
     a.scores = pass == 0 ? scores_qk : scores_kq;
     a.Ho = H; a.dil = dilation; a.S_tot = S_tot;
-    hipLaunchKernelGGL(attn_fwd_kernel<1>, dim3(a.nq * a.BH), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(attn_fwd_kernel<1>, dim3(a.nq * a.BH), dim3(64 * QW), 0, st, a);
     LH_CHECK_LAUNCH();
   }
   return LH_OK;
