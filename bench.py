@@ -2,10 +2,13 @@
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload cfg2] [--no-cpu-baseline]
 
-A step is one forward + backward of one Lighthouse layer (norm scorer) over one
-batch of seeded synthetic N(0,1) bf16 tensors already resident in HBM:
-pyramid + scores -> top-k selection -> gathered causal attention -> fan-out,
-then fan-out adjoint -> attention backward -> pyramid backward.
+A step is one forward + backward of one Lighthouse layer over one batch of
+seeded synthetic N(0,1) bf16 tensors already resident in HBM: pyramid + scores
+(norm, or dilated attention scores) -> top-k selection -> gathered causal
+attention -> fan-out, then fan-out adjoint -> attention backward -> pyramid
+backward.  The default workload is cfg2 (S=32768, H=8, k=2048, L=3, p=4,
+norm scorer), the configuration the metric is quoted on; the other workloads
+are the remaining benchmark configurations at their full sizes.
 
 Prints one JSON line.  `value` is tokens/s = B*S*steps / timed seconds.
 `roofline` is for the kernel with the largest share of the step, timed with
@@ -29,24 +32,61 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 
 WORKLOADS = {
-    # name: (B, H, S, L, p, topk, strict)
-    "cfg2": (1, 8, 32768, 3, 4, 2048, True),
-    "cfg3_k1536": (1, 8, 65536, 3, 4, 1536, False),
-    "cfg3_k3072": (1, 8, 65536, 3, 4, 3072, False),
-    "cfg3_k6144": (1, 8, 65536, 3, 4, 6144, False),
-    "cfg5_layer": (1, 8, 32768, 3, 4, 1536, False),
+    # BASELINE configs 2-4 and the Lighthouse-layer shape of config 5 (config 1 is the CPU-only case).
+    # heavy_keys: fraction of key positions (the same for every head) scaled by 4, from a seeded draw.
+    "cfg2": dict(B=1, H=8, S=32768, L=3, p=4, topk=2048, strict=True, scorer="norm"),
+    "cfg3_k1536": dict(B=1, H=8, S=65536, L=3, p=4, topk=1536, strict=False, scorer="norm", heavy_keys=0.05),
+    "cfg3_k3072": dict(B=1, H=8, S=65536, L=3, p=4, topk=3072, strict=False, scorer="norm", heavy_keys=0.05),
+    "cfg3_k6144": dict(B=1, H=8, S=65536, L=3, p=4, topk=6144, strict=False, scorer="norm", heavy_keys=0.05),
+    "cfg4": dict(B=1, H=8, S=131072, L=5, p=2, topk=1536, strict=False, scorer="dilated", dilation=4),
+    "cfg5_layer": dict(B=1, H=8, S=32768, L=3, p=4, topk=1536, strict=False, scorer="norm"),
 }
 D = 128
 
 
-def algorithmic_work(B, H, S, L, p, S_sel):
+def make_inputs(w, torch, device, seed=1234, heads=None):
+    """Seeded synthetic layer inputs of workload `w`: bf16 q, k, v [B, S, H, D]
+    and upstream grad [B, H, S, D], drawn N(0,1) in fp32 and cast.  `heads`
+    keeps a subset of the H heads (the draw is the same as for all heads)."""
+    B, H, S = w["B"], w["H"], w["S"]
+    g = torch.Generator(device=device).manual_seed(seed)
+    xs = [torch.randn(B, S, H, D, device=device, generator=g) for _ in range(3)]
+    if w.get("heavy_keys"):
+        pos = torch.randperm(S, device=device, generator=g)[: int(round(w["heavy_keys"] * S))]
+        xs[1][:, pos] *= 4.0
+    dout = torch.randn(B, H, S, D, device=device, generator=g)
+    if heads is not None:
+        hs = torch.as_tensor(heads, device=device)
+        xs = [x.index_select(2, hs) for x in xs]
+        dout = dout.index_select(1, hs)
+    return [x.bfloat16() for x in xs], dout.bfloat16()
+
+
+def make_layer(w, pkg):
+    """LighthouseLocal for workload `w`, built as the reference model builds it."""
+    if w["scorer"] == "dilated":
+        scorer = pkg.DilatedLighthouseScorer(head_dim=D, dilation=w["dilation"], pooling_factor=w["p"],
+                                             levels=w["L"])
+    else:
+        scorer = pkg.DialatedLighthouseNormScorer(pooling_factor=w["p"], levels=w["L"])
+    return pkg.LighthouseLocal(attention=None, scorer=scorer, num_levels=w["L"], pooling_factor=w["p"],
+                               topk=w["topk"], strict=w["strict"])
+
+
+def algorithmic_work(w, S_sel):
     """Per-launch algorithmic work of each native op: (kind, amount) with kind
     'bytes' (HBM-bound) or 'flop' (MFMA-bound).  bf16 = 2 bytes, fp32 = 4."""
+    B, H, S, L, p = w["B"], w["H"], w["S"], w["L"], w["p"]
     S_tot = sum(S // p ** l for l in range(L))
     pairs = S_sel * (S_sel + 1) / 2 * B * H  # causal (query, key) pairs
     e = 2
-    return {
-        "pyramid": ("bytes", 3 * S * H * D * e * B + 3 * (S_tot - S) * H * D * e * B + 2 * S_tot * H * 4 * B),
+    if w["scorer"] == "dilated":
+        # base scores come in (fp32, two tensors); pooled levels of rows and scores go out
+        pyr = 3 * S * H * D * e + 3 * (S_tot - S) * H * D * e + 2 * S * H * 4 + 2 * (S_tot - S) * H * 4
+    else:
+        pyr = 3 * S * H * D * e + 3 * (S_tot - S) * H * D * e + 2 * S_tot * H * 4
+    work = {
+        "pyramid": ("bytes", pyr * B),
         "select": ("bytes", (2 * S_sel * H * 4 + S_sel * H * 4 + S_tot * H * 4) * B),
         "attn_fwd": ("flop", 4 * D * pairs),            # S = Q K^T and O = P V
         "scatter_fwd": ("bytes", ((S_sel + S) * H * D * e + S_tot * H * 4) * B),
@@ -55,17 +95,20 @@ def algorithmic_work(B, H, S, L, p, S_sel):
         "attn_bwd_dq": ("flop", 2 * D * pairs),         # the dQ pass (S and dP are recomputed)
         "pyramid_bwd": ("bytes", (3 * S_sel * H * D * e + 3 * S * H * D * e + S_tot * H * 4) * B),
     }
+    if w["scorer"] == "dilated":
+        sd = S // w["dilation"]
+        # two dense causal attentions (q->k, k->q) over dil*H virtual heads of length S/dil
+        work["dilated_scores"] = ("flop", 2 * 4 * D * (w["dilation"] * H) * sd * (sd + 1) / 2 * B)
+    return work
 
 
 def run_gpu(args, pkg, torch):
-    B, H, S, L, p, k, strict = WORKLOADS[args.workload]
+    w = WORKLOADS[args.workload]
+    B, H, S, L, p, k, strict = (w[n] for n in ("B", "H", "S", "L", "p", "topk", "strict"))
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev).manual_seed(1234)
-    xs = [torch.randn(B, S, H, D, device=dev, generator=g).bfloat16().requires_grad_() for _ in range(3)]
-    dout = torch.randn(B, H, S, D, device=dev, generator=g).bfloat16()
-    scorer = pkg.DialatedLighthouseNormScorer(pooling_factor=p, levels=L)
-    layer = pkg.LighthouseLocal(attention=None, scorer=scorer, num_levels=L, pooling_factor=p, topk=k,
-                                strict=strict)
+    xs, dout = make_inputs(w, torch, dev)
+    xs = [x.requires_grad_() for x in xs]
+    layer = make_layer(w, pkg)
     S_sel = pkg._native.geometry(S, L, p, k, strict)[3]
 
     def step():
@@ -108,7 +151,7 @@ def run_gpu(args, pkg, torch):
             continue
         per_op.setdefault(name, []).append(prev.elapsed_time(ev))
         prev = ev
-    work = algorithmic_work(B, H, S, L, p, S_sel)
+    work = algorithmic_work(w, S_sel)
     kernels = {}
     for name, ts in per_op.items():
         avg_ms = sum(ts) / len(ts)
@@ -126,8 +169,12 @@ def run_gpu(args, pkg, torch):
                 "unit": kd["unit"], "frac": kd["frac"], "traffic": None}
     tokens_per_s = B * S / (ms_step * 1e-3)
     cfg = {"workload": f"lighthouse_layer_fwd_bwd_{args.workload}", "B": B, "H": H, "D": D, "S": S,
-           "num_levels": L, "pooling_factor": p, "topk": k, "scorer": "norm", "S_sel": S_sel,
+           "num_levels": L, "pooling_factor": p, "topk": k, "scorer": w["scorer"], "S_sel": S_sel,
            "strict": strict, "parallelism": "single GPU"}
+    if w["scorer"] == "dilated":
+        cfg["dilation"] = w["dilation"]
+    if w.get("heavy_keys"):
+        cfg["heavy_keys"] = w["heavy_keys"]
     return {
         "tokens_per_s": tokens_per_s, "ms_step": ms_step, "wall_ms_step": wall_ms_step, "config": cfg,
         "roofline": roofline, "kernels": kernels,
@@ -139,14 +186,14 @@ def run_cpu_baseline(args, torch):
     workload with `--cpu-heads` of its H heads, scaled to all heads."""
     import numpy as np
     from oracle import lh_oracle as O
-    B, H, S, L, p, k, strict = WORKLOADS[args.workload]
-    hs = max(1, min(args.cpu_heads, H))
-    g = torch.Generator().manual_seed(99)
-    xs = [torch.randn(B, S, hs, D, generator=g).bfloat16().float().requires_grad_() for _ in range(3)]
-    dout = torch.randn(B, hs, S, D, generator=g)
+    w = WORKLOADS[args.workload]
+    B, H, S, L, p, k, strict = (w[n] for n in ("B", "H", "S", "L", "p", "topk", "strict"))
+    hs = max(1, min(args.cpu_heads if args.cpu_heads else (1 if w["scorer"] == "dilated" else 4), H))
+    xs, dout = make_inputs(w, torch, torch.device("cpu"), seed=99, heads=list(range(hs)))
+    xs = [x.float().requires_grad_() for x in xs]
     t0 = time.perf_counter()
-    out, idx = O.lighthouse_layer(*xs, L, p, k, strict=strict)
-    out.backward(dout)
+    out, idx = O.lighthouse_layer(*xs, L, p, k, scorer=w["scorer"], dilation=w.get("dilation", 4), strict=strict)
+    out.backward(dout.float())
     dt = time.perf_counter() - t0
     tok_s = B * S / (dt * H / hs)
     return {"value": round(tok_s, 2), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
@@ -161,7 +208,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=4)
+    ap.add_argument("--cpu-heads", type=int, default=0, help="heads in the CPU sample (0: 4, or 1 for dilated)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU per process and has no multi-GPU path; "
@@ -184,7 +231,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: seeded N(0,1) bf16 q/k/v [B,S,H,D] and upstream grad [B,H,S,D], resident in HBM",
+        "data": "synthetic: seeded N(0,1) bf16 q/k/v [B,S,H,D] and upstream grad [B,H,S,D], resident in HBM"
+                + ("; 5% of key positions x4" if WORKLOADS[args.workload].get("heavy_keys") else ""),
         "config": r["config"],
         "roofline": r["roofline"],
         "cpu_baseline": cpu,

@@ -373,16 +373,78 @@ def norm_scorer(xq, xk, xv, pooling_factor: int = 4, levels: int = 3):
     return cat(al), cat(bl), cat(ql), cat(kl), cat(vl)
 
 
-def sdpa_causal(q, k, v, scale: float | None = None):
+_ATTN_CHUNK_ELEMS = 1 << 27  # score elements held at once by the chunked form (512 MiB fp32)
+
+
+def sdpa_causal(q, k, v, scale: float | None = None, chunk: int | None = None):
     """Causal softmax attention ``softmax(q k^T * scale + mask) v`` on
     ``[..., n, D]`` tensors (the torchtitan SDPA wrapper with ``is_causal``,
-    ``src/lighthouse_selection.py:815``), written out explicitly."""
+    ``src/lighthouse_selection.py:815``), written out explicitly.
+
+    Long sequences go through ``_ChunkedCausalAttn`` (query blocks of
+    ``chunk`` rows, default sized to ``_ATTN_CHUNK_ELEMS``), which is the same
+    formula evaluated block by block with a hand-written backward, so memory
+    stays bounded at the benchmark sizes."""
     n, dh = q.shape[-2], q.shape[-1]
     scale = 1.0 / math.sqrt(dh) if scale is None else scale
+    if chunk is None:
+        rows = max(1, q.numel() // (n * dh)) if n else 1
+        chunk = max(64, _ATTN_CHUNK_ELEMS // max(1, rows * n))
+    if chunk < n:
+        return _ChunkedCausalAttn.apply(q, k, v, scale, chunk)
     s = torch.matmul(q, k.transpose(-1, -2).contiguous()) * scale
     mask = torch.ones(n, k.shape[-2], dtype=torch.bool, device=q.device).tril()
     s = s.masked_fill(~mask, float("-inf"))
     return torch.matmul(torch.softmax(s, dim=-1), v)
+
+
+def _causal_block_scores(q, k, i0, i1, scale):
+    """Scaled, causally masked scores of queries [i0, i1) against keys [0, i1)."""
+    s = torch.matmul(q[..., i0:i1, :], k[..., :i1, :].transpose(-1, -2).contiguous()) * scale
+    above = torch.arange(i1, device=q.device)[None, :] > torch.arange(i0, i1, device=q.device)[:, None]
+    return s.masked_fill(above, float("-inf"))
+
+
+class _ChunkedCausalAttn(torch.autograd.Function if torch is not None else object):
+    """``sdpa_causal`` by query blocks: forward keeps the row log-sum-exp,
+    backward recomputes each block's probabilities from it
+    (dV += P^T dO, dP = dO V^T, dS = P (dP - rowsum(dO o O)) * scale,
+    dQ = dS K, dK += dS^T Q)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale, chunk):
+        n = q.shape[-2]
+        o = torch.empty_like(q)
+        lse = q.new_empty(q.shape[:-1])
+        for i0 in range(0, n, chunk):
+            i1 = min(n, i0 + chunk)
+            s = _causal_block_scores(q, k, i0, i1, scale)
+            m = s.amax(-1, keepdim=True)
+            e = torch.exp(s - m)
+            den = e.sum(-1, keepdim=True)
+            o[..., i0:i1, :] = torch.matmul(e, v[..., :i1, :]) / den
+            lse[..., i0:i1] = (m + torch.log(den)).squeeze(-1)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.scale, ctx.chunk = scale, chunk
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse = ctx.saved_tensors
+        scale, chunk = ctx.scale, ctx.chunk
+        n = q.shape[-2]
+        delta = (do * o).sum(-1, keepdim=True)
+        dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
+        for i0 in range(0, n, chunk):
+            i1 = min(n, i0 + chunk)
+            pr = torch.exp(_causal_block_scores(q, k, i0, i1, scale) - lse[..., i0:i1, None])
+            doc = do[..., i0:i1, :]
+            dv[..., :i1, :] += torch.matmul(pr.transpose(-1, -2).contiguous(), doc)
+            dp = torch.matmul(doc, v[..., :i1, :].transpose(-1, -2).contiguous())
+            ds = pr * (dp - delta[..., i0:i1, :]) * scale
+            dq[..., i0:i1, :] = torch.matmul(ds, k[..., :i1, :])
+            dk[..., :i1, :] += torch.matmul(ds.transpose(-1, -2).contiguous(), q[..., i0:i1, :])
+        return dq, dk, dv, None, None
 
 
 def dilated_scorer(xq, xk, xv, dilation: int = 4, pooling_factor: int = 4, levels: int = 3,
@@ -404,8 +466,9 @@ def dilated_scorer(xq, xk, xv, dilation: int = 4, pooling_factor: int = 4, level
     def unvirt(o):  # [b, dil*h, s/dil, d] -> [b, s, h, d]
         return o.transpose(1, 2).reshape(b, s, h, d)
 
-    out_qk = unvirt(attention(virt(xq), virt(xk), virt(xv)))
-    out_kq = unvirt(attention(virt(xk), virt(xq), virt(xv)))
+    with torch.no_grad():  # scores only feed the (integer) selection
+        out_qk = unvirt(attention(virt(xq), virt(xk), virt(xv)))
+        out_kq = unvirt(attention(virt(xk), virt(xq), virt(xv)))
     sqk = torch.linalg.vector_norm(out_qk, dim=-1)
     skq = torch.linalg.vector_norm(out_kq, dim=-1)
     ql, kl, vl, al, bl = [xq], [xk], [xv], [sqk], [skq]

@@ -12,7 +12,9 @@ select (structural) brute-force top-64(qk) + top-64(kq of the rest) per tile and
                     (oracle/select_ref.c) for both tie modes, strict and
                     generalized; a hand-built post-order on tiny trees
 norm / dilated      per-token loops
-sdpa_causal         torch's F.scaled_dot_product_attention and a naive loop
+sdpa_causal         torch's F.scaled_dot_product_attention and a naive loop; the
+                    chunked form (long sequences) against the explicit form,
+                    values and autograd gradients
 scatter fwd / bwd   per-entry loops; the adjoint identity
 layer backward      central finite differences in float64
 golden fixtures     committed vectors (tests/golden/) for cfg1 and a tie-heavy case
@@ -298,6 +300,20 @@ def test_sdpa_causal_vs_library_and_loop():
     i = 11
     w = torch.softmax((q[0, 1, i] @ k[0, 1, :i + 1].T) / 8 ** 0.5, -1)
     assert torch.allclose(out[0, 1, i], w @ v[0, 1, :i + 1], atol=1e-12)
+
+
+@pytest.mark.parametrize("chunk", [1, 5, 16])
+def test_sdpa_chunked_matches_explicit(chunk):
+    torch.manual_seed(5)
+    q, k, v = (torch.randn(2, 3, 17, 8, dtype=torch.float64, requires_grad=True) for _ in range(3))
+    ref = O.sdpa_causal(q, k, v, chunk=17)   # explicit form, torch autograd
+    w = torch.randn_like(ref)
+    gref = torch.autograd.grad((ref * w).sum(), (q, k, v))
+    out = O.sdpa_causal(q, k, v, chunk=chunk)
+    assert torch.allclose(out, ref, atol=1e-12)
+    got = torch.autograd.grad((out * w).sum(), (q, k, v))
+    for a, r in zip(got, gref):
+        assert torch.allclose(a, r, atol=1e-12)
 
 
 def test_dilated_scorer_bruteforce():
