@@ -102,6 +102,17 @@ def algorithmic_work(w, S_sel):
     return work
 
 
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary (FETCH_SIZE and WRITE_SIZE, each scaled by what the counter reads
+    for a plain copy of known size), or None if that kernel was not profiled."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "hbm_traffic.json")) as f:
+            return json.load(f)["bytes_per_launch"].get(workload, {}).get(kernel)
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def run_gpu(args, pkg, torch):
     w = WORKLOADS[args.workload]
     B, H, S, L, p, k, strict = (w[n] for n in ("B", "H", "S", "L", "p", "topk", "strict"))
@@ -166,7 +177,7 @@ def run_gpu(args, pkg, torch):
     kd = kernels[dom]
     roofline = {"kernel": dom, "bound": "mfma" if kd["unit"] == "TFLOP/s" else "hbm",
                 "achieved": kd["achieved"], "peak": BF16_PEAK_TFLOPS if kd["unit"] == "TFLOP/s" else HBM_PEAK_GBS,
-                "unit": kd["unit"], "frac": kd["frac"], "traffic": None}
+                "unit": kd["unit"], "frac": kd["frac"], "traffic": measured_traffic(args.workload, dom)}
     tokens_per_s = B * S / (ms_step * 1e-3)
     cfg = {"workload": f"lighthouse_layer_fwd_bwd_{args.workload}", "B": B, "H": H, "D": D, "S": S,
            "num_levels": L, "pooling_factor": p, "topk": k, "scorer": w["scorer"], "S_sel": S_sel,
@@ -209,12 +220,24 @@ def main():
     ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=0, help="heads in the CPU sample (0: 4, or 1 for dilated)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB five times (reference kernel of known "
+                         "traffic for the FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU per process and has no multi-GPU path; "
               f"--gpus {args.gpus} is not supported (use --gpus 1)", file=sys.stderr)
         sys.exit(2)
     import torch
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "launches": 5}))
+        return
     import __graft_entry__ as G
     pkg = G.load_package()
     r = run_gpu(args, pkg, torch)
