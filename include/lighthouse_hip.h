@@ -130,6 +130,8 @@ int lh_attn_fwd(const void *q, const void *k, const void *v, int64_t sb, int64_t
  * gather backward's row selection (src/lighthouse_selection.py:800-815).
  *   dout   bf16 [B, H, n, D] (from lh_scatter_bwd); lse, delta fp32 [B, H, n]
  *   dq, dk, dv bf16 [B, H, n, D] in selected order
+ * With indices, n must be >= 8 (LH_ERR_UNSUPPORTED otherwise); every selected
+ * length of a Lighthouse pyramid is.
  */
 int lh_attn_bwd(const void *q, const void *k, const void *v, int64_t sb, int64_t ss, int64_t sh,
                 const void *qp, const void *kp, const void *vp, int64_t pb, int64_t ps, int64_t ph,

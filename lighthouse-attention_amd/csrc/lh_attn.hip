@@ -152,6 +152,37 @@ __device__ __forceinline__ void g2l16(const bf16_t* g, bf16_t* lds_base) {
   __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_base, 16, 0, 0);
 }
 
+// The same direct loads (16 or 4 bytes per lane), written out so that the
+// compiler does not track them: its LDS-DMA alias analysis would otherwise
+// wait for every load in flight before reading any LDS buffer.  Callers order
+// these loads against LDS reads themselves (vmcnt waits and block barriers).
+// M0 (which the compiler reserves) is saved and restored around each load.
+__device__ __forceinline__ void g2l16_untracked(const void* g, void* lds_base) {
+  const uint32_t l = (uint32_t)(uintptr_t)(lds_void*)lds_base;
+  uint32_t t;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+      : "=&s"(t)
+      : "v"(g), "s"(l)
+      : "memory");
+}
+__device__ __forceinline__ void g2l4_untracked(const void* g, void* lds_base) {
+  const uint32_t l = (uint32_t)(uintptr_t)(lds_void*)lds_base;
+  uint32_t t;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+      : "=&s"(t)
+      : "v"(g), "s"(l)
+      : "memory");
+}
+
+// wait until at most N vector-memory operations of this wave are outstanding
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // Wave w fills rows 16w .. 16w+15 of a 64-row tile with four 1 KB direct loads
 // of 4 rows each.  The selected-row indices of those rows are loaded one tile
 // ahead (load_rows) so issuing a tile never waits on an index load.
@@ -212,6 +243,42 @@ __device__ __forceinline__ u32x4 op_tr(const bf16_t* tile, int r0, int db, int l
   const u32x2 lo = ld_tr16(tile + r * LH_D + ((ch ^ swz(r)) << 3) + sub);
   const u32x2 hi = ld_tr16(tile + (r + 8) * LH_D + ((ch ^ swz(r + 8)) << 3) + sub);
   return u32x4{lo.x, lo.y, hi.x, hi.y};
+}
+
+// Lane-constant parts of the operand addresses above, as byte offsets inside
+// a 16 KB tile, arranged so that a k-slice / column block is folded in with
+// one XOR:
+//   op_row(tile, r, c, hh)            at row ^ (c << 5), + 8192 for rows 32..63
+//   op_tr(tile, r0, db, lane) lo / hi at tr0 ^ (db << 6) and tr1 ^ (db << 6), + 256 r0
+// (the chunk swizzle is an XOR, and 2c + hh = 2c ^ hh, 4 db + C = 4 db ^ C).
+// Recomputing the few XORs per tile keeps the addresses out of long-lived registers.
+struct LaneLds {
+  uint32_t row, tr0, tr1;
+};
+
+__device__ __forceinline__ LaneLds lane_lds(int lane) {
+  const int l32 = lane & 31, hh = lane >> 5, j = lane & 15, g = lane >> 4;
+  const int rl = 4 * hh + (j >> 2), C = 2 * (g & 1) + ((j & 3) >> 1);
+  LaneLds o;
+  o.row = (uint32_t)(l32 * 256) | ((uint32_t)(swz(l32) ^ hh) << 4);
+  o.tr0 = (uint32_t)(rl * 256) | ((uint32_t)(C ^ swz(rl)) << 4) | ((uint32_t)(j & 1) << 3);
+  o.tr1 = (uint32_t)((rl + 8) * 256) | ((uint32_t)(C ^ swz(rl + 8)) << 4) | ((uint32_t)(j & 1) << 3);
+  return o;
+}
+
+// op_row of tile rows 32 qb + lane%32, k-slice c
+__device__ __forceinline__ u32x4 lds_row(const bf16_t* tile, const LaneLds& ll, int qb, int c) {
+  return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(tile) + ((ll.row ^ ((uint32_t)c << 5)) +
+                                                                                 8192u * qb));
+}
+
+// op_tr of tile rows r0 .., column block db
+__device__ __forceinline__ u32x4 lds_tr(const bf16_t* tile, const LaneLds& ll, int r0, int db) {
+  const char* t = reinterpret_cast<const char*>(tile);
+  const uint32_t x = (uint32_t)db << 6, o = 256u * r0;
+  const u32x2 a = ld_tr16(reinterpret_cast<const bf16_t*>(t + ((ll.tr0 ^ x) + o)));
+  const u32x2 b = ld_tr16(reinterpret_cast<const bf16_t*>(t + ((ll.tr1 ^ x) + o)));
+  return u32x4{a.x, a.y, b.x, b.y};
 }
 
 // 8 fp32 accumulator values v = 8*c2 .. 8*c2+7 -> bf16 B operand
@@ -496,137 +563,336 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const Attn
 }
 
 // ===========================================================================
-// backward dK, dV (key-stationary)
+// backward dK, dV (key-stationary, two roles in ping-pong)
+//
+// A block owns 128 keys: 4 wave pairs of 32 keys, the two waves of a pair on
+// one SIMD.  Wave 0-3 of a pair ("P wave") holds K and accumulates dV: in its
+// MFMA phase it forms S = Q K^T of the current 64-query tile and adds
+// P^T dO of the previous one; in its VALU phase it turns S into P and hands P
+// (bf16) to its partner through LDS.  Wave 4-7 ("dS wave") holds V and
+// accumulates dK: dP = dO V^T of the current tile and dS^T Q of the previous
+// one; in its VALU phase dS = P (dP - delta).  The dS waves run one phase
+// behind, and a block barrier closes every phase, so on each SIMD one wave
+// feeds the matrix core while the other runs its VALU work, and each wave needs
+// only half of the key-side registers.  Q/dO tiles (+ -lse, delta) rotate
+// through 4 LDS buffers; tile t is read in phases 2t .. 2t+3, and every wave
+// copies its 8 rows of tile j+2 into LDS in the VALU phase of step j (loaded
+// into registers one step earlier).  Deterministic: no atomics.
 // ===========================================================================
-__device__ __forceinline__ void dkdv_tile(floatx16 (&dka)[4], floatx16 (&dva)[4], const u32x4 (&kf)[8],
-                                          const u32x4 (&vf)[8], const bf16_t* Qs, const bf16_t* Ds, const float* Ls,
-                                          const float* Dl, int q0t, int my_k, int n, int lane, float sl2, bool mask) {
-  const int l32 = lane & 31, hh = lane >> 5;
-  // one 32-query half at a time keeps the live set to one S and one dP block
+__device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Row indices (through the selected-index map when GATHER) of the rows this
+// lane copies in a 64-row tile at row0 (wave w: rows 8w + 4i + lane/16,
+// i = 0, 1), clamped to the last row.  Gathered indices are 8 consecutive
+// entries read at a wave-uniform address with scalar loads (needs n >= 8).
+template <bool GATHER>
+__device__ __forceinline__ void tile_rows(int (&r)[2], const BhRows& m, int row0, int w, int lane) {
+  const int g = lane >> 4;
+  if (!GATHER) {
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    __builtin_amdgcn_s_setprio(1);
-    floatx16 s = mfma(op_row(Qs, qb * 32 + l32, 0, hh), kf[0], floatx16{});
-    floatx16 dp = mfma(op_row(Ds, qb * 32 + l32, 0, hh), vf[0], floatx16{});
+    for (int i = 0; i < 2; ++i) r[i] = min(row0 + 8 * w + 4 * i + g, m.last);
+    return;
+  }
+  const int first = __builtin_amdgcn_readfirstlane(row0 + 8 * w);
+  const int base = min(first, m.last - 7);
+  // the index map is read-only here: reading it through the constant address
+  // space lets the loads be scalar
+  typedef const __attribute__((address_space(4))) int cint;
+  cint* p = (cint*)(m.idx + base);
+  int v[8];
 #pragma unroll
-    for (int c = 1; c < 8; ++c) {
-      s = mfma(op_row(Qs, qb * 32 + l32, c, hh), kf[c], s);
-      dp = mfma(op_row(Ds, qb * 32 + l32, c, hh), vf[c], dp);
+  for (int k = 0; k < 8; ++k) v[k] = p[k];
+  if (first + 7 <= m.last) {  // no clamping: row 4i + g is entry 4i + g
+#pragma unroll
+    for (int i = 0; i < 2; ++i) r[i] = g == 0 ? v[4 * i] : g == 1 ? v[4 * i + 1] : g == 2 ? v[4 * i + 2] : v[4 * i + 3];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int k = min(first + 4 * i + g, m.last) - base;
+      int x = v[0];
+#pragma unroll
+      for (int kk = 1; kk < 8; ++kk) x = k == kk ? v[kk] : x;
+      r[i] = x;
     }
-    __builtin_amdgcn_s_setprio(0);
-    if (mask) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int q = q0t + qb * 32 + slot_key(v, hh);
-        if (my_k > q || q >= n) s[v] = -INFINITY;
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int qi = qb * 32 + 8 * g + 4 * hh;
-      const float4 l4 = *reinterpret_cast<const float4*>(Ls + qi);  // holds -lse
-      const float4 d4 = *reinterpret_cast<const float4*>(Dl + qi);
-      const float nl[4] = {l4.x, l4.y, l4.z, l4.w};
-      const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int v = 4 * g + e;
-        const float p = ex2(fmaf(s[v], sl2, nl[e]));
-        s[v] = p;
-        dp[v] = p * (dp[v] - dd[e]);
-      }
-    }
-    const u32x4 p0 = pack_frag(s, 0), p1 = pack_frag(s, 1);
-    const u32x4 s0 = pack_frag(dp, 0), s1 = pack_frag(dp, 1);
-    __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      dva[d] = mfma(op_tr(Ds, qb * 32, d, lane), p0, dva[d]);
-      dva[d] = mfma(op_tr(Ds, qb * 32 + 16, d, lane), p1, dva[d]);
-      dka[d] = mfma(op_tr(Qs, qb * 32, d, lane), s0, dka[d]);
-      dka[d] = mfma(op_tr(Qs, qb * 32 + 16, d, lane), s1, dka[d]);
-    }
-    __builtin_amdgcn_s_setprio(0);
   }
 }
 
-__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_kernel(const AttnArgs a) {
-  __shared__ __attribute__((aligned(1024))) bf16_t Q0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t Q1[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t D0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t D1[TILE];
-  __shared__ __attribute__((aligned(16))) float L0[2 * BN];  // -lse then delta
-  __shared__ __attribute__((aligned(16))) float L1[2 * BN];
+// Direct loads of this wave's 8 rows of a Q tile (gathered) and dO tile
+// (dense), plus the tile's lse (wave 0) or delta (wave 4): 4 or 5 loads.
+__device__ __forceinline__ void issue_qd(bf16_t* qt, bf16_t* dt, float* lt, const BhRows& m, const int (&r)[2],
+                                         const AttnArgs& a, int64_t bhn, int row0, int n, int w, int lane) {
+  const bf16_t* dbase = a.dout + bhn * LH_D;
+  const int rsub = lane >> 4, slot = lane & 15;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = 8 * w + 4 * i + rsub;
+    const int chunk = 8 * (slot ^ swz(row));
+    const bool pooled = r[i] >= m.split;
+    const uint32_t rel = (uint32_t)(r[i] - (pooled ? m.split : 0));
+    g2l16_untracked((pooled ? m.qp : m.q) + rel * (uint32_t)(pooled ? m.ps : m.ss) + chunk,
+                    qt + (8 * w + 4 * i) * LH_D);
+    g2l16_untracked(dbase + (uint32_t)min(row0 + row, n - 1) * LH_D + chunk, dt + (8 * w + 4 * i) * LH_D);
+  }
+  if (w == 0) g2l4_untracked(a.lse_in + bhn + min(row0 + lane, n - 1), lt);
+  if (w == 4) g2l4_untracked(a.delta + bhn + min(row0 + lane, n - 1), lt + BN);
+}
+
+#define SCHED_GROUP(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+constexpr int SG_MFMA = 0x008, SG_DSR = 0x100;
+
+// Issue order of an MFMA phase built as: 16 transposing reads (8 operands),
+// 16 more, their 8 + 8 MFMAs, 8 + 8 row reads, their 8 + 8 MFMAs.  Each
+// operand group is read while the previous group's MFMAs run, so LDS latency
+// overlaps the matrix core and at most two operand groups are live.
+__device__ __forceinline__ void mma_phase_order() {
+  SCHED_GROUP(SG_DSR, 16);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    SCHED_GROUP(SG_DSR, 2);
+    SCHED_GROUP(SG_MFMA, 1);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    SCHED_GROUP(SG_DSR, 1);
+    SCHED_GROUP(SG_MFMA, 1);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    SCHED_GROUP(SG_DSR, 1);
+    SCHED_GROUP(SG_MFMA, 1);
+  }
+  SCHED_GROUP(SG_MFMA, 8);
+}
+
+// MFMA phase of a P wave: dV += dO^T P of the previous tile (Dp, pp), then
+// S of the current tile (Qc).  Operands are read a group ahead of their MFMAs.
+__device__ __forceinline__ void pw_mma(floatx16 (&s)[2], floatx16 (&dva)[4], const u32x4 (&kf)[8],
+                                       const u32x4 (&pp)[2][2], const bf16_t* Qc, const bf16_t* Dp,
+                                       const LaneLds& ll) {
+  u32x4 oa[8], ob[8], ka[8], kb[8];
+  // operand i: rows 32 qb + 16 c2 with qb = i & 1, c2 = (i >> 1) & 1; column block db = i >> 2 (+2)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) oa[i] = lds_tr(Dp, ll, 32 * (i & 1) + 16 * ((i >> 1) & 1), i >> 2);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ob[i] = lds_tr(Dp, ll, 32 * (i & 1) + 16 * ((i >> 1) & 1), 2 + (i >> 2));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dva[i >> 2] = mfma(oa[i], pp[i & 1][(i >> 1) & 1], dva[i >> 2]);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) ka[c] = lds_row(Qc, ll, 0, c);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dva[2 + (i >> 2)] = mfma(ob[i], pp[i & 1][(i >> 1) & 1], dva[2 + (i >> 2)]);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) kb[c] = lds_row(Qc, ll, 1, c);
+  s[0] = mfma(ka[0], kf[0], floatx16{});
+#pragma unroll
+  for (int c = 1; c < 8; ++c) s[0] = mfma(ka[c], kf[c], s[0]);
+  s[1] = mfma(kb[0], kf[0], floatx16{});
+#pragma unroll
+  for (int c = 1; c < 8; ++c) s[1] = mfma(kb[c], kf[c], s[1]);
+
+  mma_phase_order();
+}
+
+// MFMA phase of a dS wave: dK += Q^T dS of the previous tile (Qp, dsf), then
+// dP of the current tile (Dc).
+__device__ __forceinline__ void dw_mma(floatx16 (&dp)[2], floatx16 (&dka)[4], const u32x4 (&vf)[8],
+                                       const u32x4 (&dsf)[2][2], const bf16_t* Dc, const bf16_t* Qp,
+                                       const LaneLds& ll) {
+  u32x4 oa[8], ob[8], ka[8], kb[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) oa[i] = lds_tr(Qp, ll, 32 * (i & 1) + 16 * ((i >> 1) & 1), i >> 2);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ob[i] = lds_tr(Qp, ll, 32 * (i & 1) + 16 * ((i >> 1) & 1), 2 + (i >> 2));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dka[i >> 2] = mfma(oa[i], dsf[i & 1][(i >> 1) & 1], dka[i >> 2]);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) ka[c] = lds_row(Dc, ll, 0, c);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dka[2 + (i >> 2)] = mfma(ob[i], dsf[i & 1][(i >> 1) & 1], dka[2 + (i >> 2)]);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) kb[c] = lds_row(Dc, ll, 1, c);
+  dp[0] = mfma(ka[0], vf[0], floatx16{});
+#pragma unroll
+  for (int c = 1; c < 8; ++c) dp[0] = mfma(ka[c], vf[c], dp[0]);
+  dp[1] = mfma(kb[0], vf[0], floatx16{});
+#pragma unroll
+  for (int c = 1; c < 8; ++c) dp[1] = mfma(kb[c], vf[c], dp[1]);
+
+  mma_phase_order();
+}
+
+template <bool GATHER>
+__global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a) {
+  __shared__ __attribute__((aligned(1024))) bf16_t Q0[TILE], Q1[TILE], Q2[TILE], Q3[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t D0[TILE], D1[TILE], D2[TILE], D3[TILE];
+  __shared__ __attribute__((aligned(16))) float L0[2 * BN], L1[2 * BN], L2[2 * BN], L3[2 * BN];  // lse, delta
+  __shared__ u32x4 EX[4][4][64];  // P handed from each P wave to its dS wave
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, pair = wave & 3;
+  const LaneLds ll = lane_lds(lane);
   int bh, kblk;
   schedule(blockIdx.x, a.nq, a.BH, bh, kblk, false);  // early key blocks see the most queries
   const int n = a.n;
   const BhRows m = bh_rows(a, bh);
-  const int k0 = kblk * BMK, kw = k0 + wave * 32, my_k = kw + l32;
+  const int k0 = kblk * BMK, kw = k0 + 32 * pair, my_k = kw + l32;
 
-  u32x4 kf[8], vf[8];
+  u32x4 kf[8];  // K (P wave) or V (dS wave) rows of this lane's key
   {
     bool pooled;
     const uint32_t o = row_off(m, my_k, pooled) + 8 * hh;
-    const bf16_t* pk = (pooled ? m.kp : m.k) + o;
-    const bf16_t* pv = (pooled ? m.vp : m.v) + o;
+    const bf16_t* p = grp ? (pooled ? m.vp : m.v) + o : (pooled ? m.kp : m.k) + o;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      kf[c] = ldg16(pk + 16 * c);
-      vf[c] = ldg16(pv + 16 * c);
-    }
+    for (int c = 0; c < 8; ++c) kf[c] = ldg16(p + 16 * c);
   }
-
-  const int jt0 = k0 / BN;
+  const int64_t bhn = (int64_t)bh * n;
+  const int jt0 = k0 / BN;  // first query tile that sees these keys
   const int nt = (n + BN - 1) / BN;
-  const bf16_t* dbase = a.dout + (int64_t)bh * n * LH_D;
-  const float* lrow = a.lse_in + (int64_t)bh * n;
-  const float* drow = a.delta + (int64_t)bh * n;
-  // threads 0..63 carry -lse, 64..127 delta of the tile's 64 queries
-  auto load_ld = [&](int q0t) -> float {
-    if (tid >= 2 * BN) return 0.f;
-    const int qq = min(q0t + (tid & (BN - 1)), n - 1);
-    return tid < BN ? -lrow[qq] : drow[qq];
-  };
-  int rr[4];
-  load_rows<4>(rr, m, jt0 * BN, wave, lane);
-  issue_rows<4>(Q0, m.q, m.qp, nullptr, nullptr, nullptr, m, rr, wave, lane);
-  issue_dense<4>(D0, dbase, n - 1, jt0 * BN, wave, lane);
-  if (tid < 2 * BN) L0[tid] = load_ld(jt0 * BN);
-  load_rows<4>(rr, m, (jt0 + 1) * BN, wave, lane);
-  wait_loads();
-  __syncthreads();
 
-  floatx16 dka[4], dva[4];
-#pragma unroll
-  for (int d = 0; d < 4; ++d) { dka[d] = floatx16{}; dva[d] = floatx16{}; }
-  // query tiles whose 64 queries are all >= this wave's last key and < n need no mask
-  const int jfull = (kw + 31 + BN - 1) / BN;
-
-  auto step = [&](int j, const bf16_t* Qs, const bf16_t* Ds, const float* Ls, bf16_t* Qn, bf16_t* Dn, float* Ln) {
-    const int q0t = j * BN;
-    float lv = 0.f;
-    if (j + 1 < nt) {
-      issue_rows<4>(Qn, m.q, m.qp, nullptr, nullptr, nullptr, m, rr, wave, lane);
-      issue_dense<4>(Dn, dbase, n - 1, q0t + BN, wave, lane);
-      lv = load_ld(q0t + BN);
+  // Each wave copies rows 8w .. 8w+7 of every tile (the P waves the first
+  // half, the dS waves the second).  Tiles jt0 and jt0+1 first, and the dS
+  // waves' half of tile jt0+2.
+  int rr[2];
+  {
+    int r1[2];
+    tile_rows<GATHER>(rr, m, jt0 * BN, wave, lane);
+    tile_rows<GATHER>(r1, m, (jt0 + 1) * BN, wave, lane);
+    issue_qd(Q0, D0, L0, m, rr, a, bhn, jt0 * BN, n, wave, lane);
+    issue_qd(Q1, D1, L1, m, r1, a, bhn, (jt0 + 1) * BN, n, wave, lane);
+    tile_rows<GATHER>(rr, m, (jt0 + 2) * BN, wave, lane);
+    if (grp) {
+      issue_qd(Q2, D2, L2, m, rr, a, bhn, (jt0 + 2) * BN, n, wave, lane);
+      tile_rows<GATHER>(rr, m, (jt0 + 3) * BN, wave, lane);
     }
-    if (j + 2 < nt) load_rows<4>(rr, m, q0t + 2 * BN, wave, lane);
-    if (j < nt && q0t + BN - 1 >= kw)
-      dkdv_tile(dka, dva, kf, vf, Qs, Ds, Ls, Ls + BN, q0t, my_k, n, lane, a.sl2, !(j >= jfull && q0t + BN <= n));
-    if (j + 1 < nt && tid < 2 * BN) Ln[tid] = lv;
-    wait_loads();
-    __syncthreads();
-  };
-  for (int j = jt0; j < nt; j += 2) {
-    step(j, Q0, D0, L0, Q1, D1, L1);
-    step(j + 1, Q1, D1, L1, Q0, D0, L0);
   }
+  // the first step's dV / dK terms multiply zeros with buffer 3: make it finite
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    reinterpret_cast<u32x4*>(Q3)[tid + 512 * i] = u32x4{};
+    reinterpret_cast<u32x4*>(D3)[tid + 512 * i] = u32x4{};
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the first tiles and the zeros are in LDS
+  block_barrier();
+
+  floatx16 acc[4];  // dV (P wave) or dK (dS wave)
+#pragma unroll
+  for (int d = 0; d < 4; ++d) acc[d] = floatx16{};
+  floatx16 sc[2] = {floatx16{}, floatx16{}};  // S (P wave) or dP (dS wave)
+  u32x4 op[2][2] = {{u32x4{}, u32x4{}}, {u32x4{}, u32x4{}}};  // P or dS, bf16 operands
+  const float sl2 = a.sl2;
+
+  // Step j: MFMA phase (tile j, and the previous tile's accumulation), then
+  // VALU phase.  In its VALU phase a P wave issues its half of tile j+2 (into
+  // the buffer of tile j-2, last read in phase 2j-1) and a dS wave its half of
+  // tile j+3 (buffer of tile j-1, last read in phase 2j+1); each wave keeps
+  // one step's loads in flight and waits for the older ones before the barrier
+  // ahead of the phase that reads them (P waves at the end of their VALU
+  // phase, dS waves at the end of their MFMA phase).  The step count is
+  // rounded up to a multiple of 4 so that the buffers rotate statically; steps
+  // past the last tile copy clamped rows, so every step issues the same loads.
+  // Each role runs its own loop (same barrier count) and is register-allocated
+  // on its own.
+  // loads one wave issues per step: 4 row groups, + lse (wave 0) or delta (wave 4)
+  const bool ld5 = (wave & 3) == 0;
+  auto wait_prev_step = [&]() {
+    if (ld5)
+      wait_vm<5>();
+    else
+      wait_vm<4>();
+  };
+  auto pstep = [&](int j, const bf16_t* Qc, const float* Lc, const bf16_t* Dp, bf16_t* Qn, bf16_t* Dn, float* Ln) {
+    __builtin_amdgcn_s_setprio(1);
+    pw_mma(sc, acc, kf, op, Qc, Dp, ll);
+    __builtin_amdgcn_s_setprio(0);
+    block_barrier();
+    issue_qd(Qn, Dn, Ln, m, rr, a, bhn, (j + 2) * BN, n, wave, lane);
+    tile_rows<GATHER>(rr, m, (j + 3) * BN, wave, lane);
+    if (j < nt) {  // P = exp2(S sl2 - lse), masked causally and past n
+      const int q0t = j * BN;
+      const bool mask = q0t < kw + 31 || q0t + BN > n;
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        if (mask) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int q = q0t + qb * 32 + slot_key(v, hh);
+            if (my_k > q || q >= n) sc[qb][v] = -INFINITY;
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 l4 = *reinterpret_cast<const float4*>(Lc + qb * 32 + 8 * g + 4 * hh);  // lse
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sc[qb][4 * g + e] = ex2(fmaf(sc[qb][4 * g + e], sl2, -lv[e]));
+        }
+        op[qb][0] = pack_frag(sc[qb], 0);
+        op[qb][1] = pack_frag(sc[qb], 1);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) EX[pair][i][lane] = op[i >> 1][i & 1];
+    } else {  // past the last tile the accumulation steps add zeros
+      op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this phase's LDS writes have landed
+    wait_prev_step();                    // tile j+1 has landed
+    block_barrier();
+  };
+  auto dstep = [&](int j, const bf16_t* Dc, const float* Lc, const bf16_t* Qp, bf16_t* Qn, bf16_t* Dn, float* Ln) {
+    __builtin_amdgcn_s_setprio(1);
+    dw_mma(sc, acc, kf, op, Dc, Qp, ll);
+    __builtin_amdgcn_s_setprio(0);
+    wait_prev_step();  // tile j+1 has landed
+    block_barrier();
+    issue_qd(Qn, Dn, Ln, m, rr, a, bhn, (j + 3) * BN, n, wave, lane);
+    tile_rows<GATHER>(rr, m, (j + 4) * BN, wave, lane);
+    if (j < nt) {  // dS = P (dP - delta), P from the partner P wave
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const u32x4 e0 = EX[pair][2 * qb][lane], e1 = EX[pair][2 * qb + 1][lane];
+        float pv[16];
+        unpack8(uint4{e0.x, e0.y, e0.z, e0.w}, pv);
+        unpack8(uint4{e1.x, e1.y, e1.z, e1.w}, pv + 8);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 d4 = *reinterpret_cast<const float4*>(Lc + BN + qb * 32 + 8 * g + 4 * hh);  // delta
+          const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sc[qb][4 * g + e] = pv[4 * g + e] * (sc[qb][4 * g + e] - dd[e]);
+        }
+        op[qb][0] = pack_frag(sc[qb], 0);
+        op[qb][1] = pack_frag(sc[qb], 1);
+      }
+    } else {
+      op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the partner's P has been read
+    block_barrier();
+  };
+  if (grp == 0) {
+    for (int j = jt0; j <= nt; j += 4) {
+      pstep(j, Q0, L0, D3, Q2, D2, L2);
+      pstep(j + 1, Q1, L1, D0, Q3, D3, L3);
+      pstep(j + 2, Q2, L2, D1, Q0, D0, L0);
+      pstep(j + 3, Q3, L3, D2, Q1, D1, L1);
+    }
+    block_barrier();
+  } else {
+    block_barrier();  // the dS waves run one phase behind
+    for (int j = jt0; j <= nt; j += 4) {
+      dstep(j, D0, L0, Q3, Q3, D3, L3);
+      dstep(j + 1, D1, L1, Q0, Q0, D0, L0);
+      dstep(j + 2, D2, L2, Q1, Q1, D1, L1);
+      dstep(j + 3, D3, L3, Q2, Q2, D2, L2);
+    }
+  }
+  wait_vm<0>();  // no direct-to-LDS load may outlive the block
 
   if (my_k >= n) return;
-  store_rows_bf16(a.dk + ((int64_t)bh * n + my_k) * LH_D, dka, a.scale, hh);
-  store_rows_bf16(a.dv + ((int64_t)bh * n + my_k) * LH_D, dva, 1.0f, hh);
+  if (grp == 0)
+    store_rows_bf16(a.dv + ((int64_t)bh * n + my_k) * LH_D, acc, 1.0f, hh);
+  else
+    store_rows_bf16(a.dk + ((int64_t)bh * n + my_k) * LH_D, acc, a.scale, hh);
 }
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -686,6 +952,7 @@ int attn_bwd_parts(int parts, const void* q, const void* k, const void* v, int64
   int rc = fill_rows(a, q, k, v, sb, ss, sh, qp, kp, vp, pb, ps, ph, split, indices, B, H, n, D, scale);
   if (rc) return rc;
   if (!dout || !lse || !delta || !al16(dout)) return LH_ERR_INVALID_ARG;
+  if (indices && n < 8) return LH_ERR_UNSUPPORTED;  // gathered rows are indexed 8 at a time
   if ((parts & 1) && (!dk || !dv || !al16(dk) || !al16(dv))) return LH_ERR_INVALID_ARG;
   if ((parts & 2) && (!dq || !al16(dq))) return LH_ERR_INVALID_ARG;
   a.dout = (const bf16_t*)dout; a.lse_in = lse; a.delta = delta;
@@ -694,7 +961,10 @@ int attn_bwd_parts(int parts, const void* q, const void* k, const void* v, int64
   if (parts & 1) {
     AttnArgs ak = a;
     ak.nq = (a.n + BMK - 1) / BMK;
-    hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(ak.nq * ak.BH), dim3(256), 0, st, ak);
+    if (indices)
+      hipLaunchKernelGGL(attn_bwd_dkdv_kernel<true>, dim3(ak.nq * ak.BH), dim3(512), 0, st, ak);
+    else
+      hipLaunchKernelGGL(attn_bwd_dkdv_kernel<false>, dim3(ak.nq * ak.BH), dim3(512), 0, st, ak);
     LH_CHECK_LAUNCH();
   }
   if (parts & 2) {
