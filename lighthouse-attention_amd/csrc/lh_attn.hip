@@ -152,30 +152,6 @@ __device__ __forceinline__ void g2l16(const bf16_t* g, bf16_t* lds_base) {
   __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_base, 16, 0, 0);
 }
 
-// The same direct loads (16 or 4 bytes per lane), written out so that the
-// compiler does not track them: its LDS-DMA alias analysis would otherwise
-// wait for every load in flight before reading any LDS buffer.  Callers order
-// these loads against LDS reads themselves (vmcnt waits and block barriers).
-// M0 (which the compiler reserves) is saved and restored around each load.
-__device__ __forceinline__ void g2l16_untracked(const void* g, void* lds_base) {
-  const uint32_t l = (uint32_t)(uintptr_t)(lds_void*)lds_base;
-  uint32_t t;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-      : "=&s"(t)
-      : "v"(g), "s"(l)
-      : "memory");
-}
-__device__ __forceinline__ void g2l4_untracked(const void* g, void* lds_base) {
-  const uint32_t l = (uint32_t)(uintptr_t)(lds_void*)lds_base;
-  uint32_t t;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-      : "=&s"(t)
-      : "v"(g), "s"(l)
-      : "memory");
-}
-
 // wait until at most N vector-memory operations of this wave are outstanding
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -617,24 +593,47 @@ __device__ __forceinline__ void tile_rows(int (&r)[2], const BhRows& m, int row0
   }
 }
 
-// Direct loads of this wave's 8 rows of a Q tile (gathered) and dO tile
-// (dense), plus the tile's lse (wave 0) or delta (wave 4): 4 or 5 loads.
-__device__ __forceinline__ void issue_qd(bf16_t* qt, bf16_t* dt, float* lt, const BhRows& m, const int (&r)[2],
-                                         const AttnArgs& a, int64_t bhn, int row0, int n, int w, int lane) {
-  const bf16_t* dbase = a.dout + bhn * LH_D;
+// This wave's 8 rows of a Q tile (gathered) and dO tile (dense), plus the
+// tile's lse (wave 0) or delta (wave 4), staged in registers: loaded at the
+// start of a VALU phase and written to LDS at its end, so the loads' latency
+// is covered by the phase's VALU work and no load is in flight across a
+// barrier.
+struct QdRegs {
+  u32x4 q[2], d[2];
+  float ld;
+};
+
+__device__ __forceinline__ void load_qd(QdRegs& x, const BhRows& m, const int (&r)[2], const AttnArgs& a,
+                                        int64_t bhn, int row0, int n, int w, int lane) {
   const int rsub = lane >> 4, slot = lane & 15;
+  const bf16_t* dbase = a.dout + bhn * LH_D;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int row = 8 * w + 4 * i + rsub;
     const int chunk = 8 * (slot ^ swz(row));
     const bool pooled = r[i] >= m.split;
     const uint32_t rel = (uint32_t)(r[i] - (pooled ? m.split : 0));
-    g2l16_untracked((pooled ? m.qp : m.q) + rel * (uint32_t)(pooled ? m.ps : m.ss) + chunk,
-                    qt + (8 * w + 4 * i) * LH_D);
-    g2l16_untracked(dbase + (uint32_t)min(row0 + row, n - 1) * LH_D + chunk, dt + (8 * w + 4 * i) * LH_D);
+    x.q[i] = ldg16((pooled ? m.qp : m.q) + rel * (uint32_t)(pooled ? m.ps : m.ss) + chunk);
+    x.d[i] = ldg16(dbase + (uint32_t)min(row0 + row, n - 1) * LH_D + chunk);
   }
-  if (w == 0) g2l4_untracked(a.lse_in + bhn + min(row0 + lane, n - 1), lt);
-  if (w == 4) g2l4_untracked(a.delta + bhn + min(row0 + lane, n - 1), lt + BN);
+  if (w == 0) x.ld = a.lse_in[bhn + min(row0 + lane, n - 1)];
+  if (w == 4) x.ld = a.delta[bhn + min(row0 + lane, n - 1)];
+}
+
+__device__ __forceinline__ void store_qd(bf16_t* qt, bf16_t* dt, float* lt, const QdRegs& x, int w, int lane) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    *reinterpret_cast<u32x4*>(qt + (8 * w + 4 * i) * LH_D + 8 * lane) = x.q[i];
+    *reinterpret_cast<u32x4*>(dt + (8 * w + 4 * i) * LH_D + 8 * lane) = x.d[i];
+  }
+  if (w == 0) lt[lane] = x.ld;
+  if (w == 4) lt[BN + lane] = x.ld;
+}
+
+// this lane's gathered row indices (rows 8w + 4i + lane/16) of a tile, clamped
+__device__ __forceinline__ void load_rows8(int (&r)[2], const BhRows& m, int row0, int w, int lane) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) r[i] = m.idx[min(row0 + 8 * w + 4 * i + (lane >> 4), m.last)];
 }
 
 #define SCHED_GROUP(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
@@ -750,20 +749,27 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
   const int nt = (n + BN - 1) / BN;
 
   // Each wave copies rows 8w .. 8w+7 of every tile (the P waves the first
-  // half, the dS waves the second).  Tiles jt0 and jt0+1 first, and the dS
-  // waves' half of tile jt0+2.
-  int rr[2];
+  // half, the dS waves the second).  In step j the P waves copy tile j+2 and
+  // the dS waves tile j+3 (lead); tiles jt0, jt0+1 (and the dS waves' half of
+  // jt0+2) are copied here.
+  const int lead = grp ? 3 : 2;
+  int rr[2];  // row indices of the next tile this wave copies
   {
-    int r1[2];
-    tile_rows<GATHER>(rr, m, jt0 * BN, wave, lane);
-    tile_rows<GATHER>(r1, m, (jt0 + 1) * BN, wave, lane);
-    issue_qd(Q0, D0, L0, m, rr, a, bhn, jt0 * BN, n, wave, lane);
-    issue_qd(Q1, D1, L1, m, r1, a, bhn, (jt0 + 1) * BN, n, wave, lane);
-    tile_rows<GATHER>(rr, m, (jt0 + 2) * BN, wave, lane);
-    if (grp) {
-      issue_qd(Q2, D2, L2, m, rr, a, bhn, (jt0 + 2) * BN, n, wave, lane);
-      tile_rows<GATHER>(rr, m, (jt0 + 3) * BN, wave, lane);
+    QdRegs x;
+    for (int t = jt0; t < jt0 + lead; ++t) {
+      if (GATHER)
+        load_rows8(rr, m, t * BN, wave, lane);
+      else
+        tile_rows<false>(rr, m, t * BN, wave, lane);
+      load_qd(x, m, rr, a, bhn, t * BN, n, wave, lane);
+      const int b = t - jt0;
+      store_qd(b == 0 ? Q0 : b == 1 ? Q1 : Q2, b == 0 ? D0 : b == 1 ? D1 : D2, b == 0 ? L0 : b == 1 ? L1 : L2, x,
+               wave, lane);
     }
+    if (GATHER)
+      load_rows8(rr, m, (jt0 + lead) * BN, wave, lane);
+    else
+      tile_rows<false>(rr, m, (jt0 + lead) * BN, wave, lane);
   }
   // the first step's dV / dK terms multiply zeros with buffer 3: make it finite
 #pragma unroll
@@ -771,7 +777,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
     reinterpret_cast<u32x4*>(Q3)[tid + 512 * i] = u32x4{};
     reinterpret_cast<u32x4*>(D3)[tid + 512 * i] = u32x4{};
   }
-  __builtin_amdgcn_s_waitcnt(0);  // the first tiles and the zeros are in LDS
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the first tiles and the zeros are in LDS
   block_barrier();
 
   floatx16 acc[4];  // dV (P wave) or dK (dS wave)
@@ -782,31 +788,28 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
   const float sl2 = a.sl2;
 
   // Step j: MFMA phase (tile j, and the previous tile's accumulation), then
-  // VALU phase.  In its VALU phase a P wave issues its half of tile j+2 (into
-  // the buffer of tile j-2, last read in phase 2j-1) and a dS wave its half of
-  // tile j+3 (buffer of tile j-1, last read in phase 2j+1); each wave keeps
-  // one step's loads in flight and waits for the older ones before the barrier
-  // ahead of the phase that reads them (P waves at the end of their VALU
-  // phase, dS waves at the end of their MFMA phase).  The step count is
-  // rounded up to a multiple of 4 so that the buffers rotate statically; steps
-  // past the last tile copy clamped rows, so every step issues the same loads.
-  // Each role runs its own loop (same barrier count) and is register-allocated
-  // on its own.
-  // loads one wave issues per step: 4 row groups, + lse (wave 0) or delta (wave 4)
-  const bool ld5 = (wave & 3) == 0;
-  auto wait_prev_step = [&]() {
-    if (ld5)
-      wait_vm<5>();
+  // VALU phase, which also copies tile j + lead into the buffer of tile
+  // j + lead - 4 (last read in phase 2j-1 by a P wave's copy, 2j+1 by a dS
+  // wave's); the copies land before the phase's closing barrier.  The step
+  // count is rounded up to a multiple of 4 so that the buffers rotate
+  // statically; steps past the last tile copy clamped rows.  Each role runs its
+  // own loop (same barrier count) and is register-allocated on its own.
+  QdRegs xs;
+  auto copy_begin = [&](int j) {
+    const int t = j + lead;
+    load_qd(xs, m, rr, a, bhn, t * BN, n, wave, lane);
+    if (GATHER)
+      load_rows8(rr, m, (t + 1) * BN, wave, lane);
     else
-      wait_vm<4>();
+      tile_rows<false>(rr, m, (t + 1) * BN, wave, lane);
   };
+  auto copy_end = [&](bf16_t* Qn, bf16_t* Dn, float* Ln) { store_qd(Qn, Dn, Ln, xs, wave, lane); };
   auto pstep = [&](int j, const bf16_t* Qc, const float* Lc, const bf16_t* Dp, bf16_t* Qn, bf16_t* Dn, float* Ln) {
     __builtin_amdgcn_s_setprio(1);
     pw_mma(sc, acc, kf, op, Qc, Dp, ll);
     __builtin_amdgcn_s_setprio(0);
     block_barrier();
-    issue_qd(Qn, Dn, Ln, m, rr, a, bhn, (j + 2) * BN, n, wave, lane);
-    tile_rows<GATHER>(rr, m, (j + 3) * BN, wave, lane);
+    copy_begin(j);
     if (j < nt) {  // P = exp2(S sl2 - lse), masked causally and past n
       const int q0t = j * BN;
       const bool mask = q0t < kw + 31 || q0t + BN > n;
@@ -834,18 +837,16 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
     } else {  // past the last tile the accumulation steps add zeros
       op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
     }
+    copy_end(Qn, Dn, Ln);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this phase's LDS writes have landed
-    wait_prev_step();                    // tile j+1 has landed
     block_barrier();
   };
   auto dstep = [&](int j, const bf16_t* Dc, const float* Lc, const bf16_t* Qp, bf16_t* Qn, bf16_t* Dn, float* Ln) {
     __builtin_amdgcn_s_setprio(1);
     dw_mma(sc, acc, kf, op, Dc, Qp, ll);
     __builtin_amdgcn_s_setprio(0);
-    wait_prev_step();  // tile j+1 has landed
     block_barrier();
-    issue_qd(Qn, Dn, Ln, m, rr, a, bhn, (j + 3) * BN, n, wave, lane);
-    tile_rows<GATHER>(rr, m, (j + 4) * BN, wave, lane);
+    copy_begin(j);
     if (j < nt) {  // dS = P (dP - delta), P from the partner P wave
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
@@ -866,7 +867,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
     } else {
       op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the partner's P has been read
+    copy_end(Qn, Dn, Ln);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the copies have landed, the partner's P was read
     block_barrier();
   };
   if (grp == 0) {
@@ -886,8 +888,6 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
       dstep(j + 3, D3, L3, Q2, Q2, D2, L2);
     }
   }
-  wait_vm<0>();  // no direct-to-LDS load may outlive the block
-
   if (my_k >= n) return;
   if (grp == 0)
     store_rows_bf16(a.dv + ((int64_t)bh * n + my_k) * LH_D, acc, 1.0f, hh);
