@@ -8,7 +8,9 @@ seeded synthetic N(0,1) bf16 tensors already resident in HBM: pyramid + scores
 attention -> fan-out, then fan-out adjoint -> attention backward -> pyramid
 backward.  The default workload is cfg2 (S=32768, H=8, k=2048, L=3, p=4,
 norm scorer), the configuration the metric is quoted on; the other workloads
-are the remaining benchmark configurations at their full sizes.
+are the remaining benchmark configurations at their full sizes.  The model
+workload cfg5 times one training step of the Llama3 270M Lighthouse model
+instead (forward, backward, gradient clipping, AdamW).
 
 Prints one JSON line.  `value` is tokens/s = B*S*steps / timed seconds.
 `roofline` is for the kernel with the largest share of the step, timed with
@@ -30,6 +32,7 @@ sys.path.insert(0, ROOT)
 METRIC = "Lighthouse layer fwd+bwd tokens/s at S=32K,k=2048 bf16; % HBM/MFMA roofline"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+MODEL_METRIC = "Llama3 270M Lighthouse training step tokens/s (fwd+bwd+AdamW), S=32K, bf16"
 
 WORKLOADS = {
     # BASELINE configs 2-4 and the Lighthouse-layer shape of config 5 (config 1 is the CPU-only case).
@@ -42,6 +45,13 @@ WORKLOADS = {
     "cfg5_layer": dict(B=1, H=8, S=32768, L=3, p=4, topk=1536, strict=False, scorer="norm"),
 }
 D = 128
+# Model workloads: one training step (forward, backward, clip, AdamW) of the Llama3 model.
+MODEL_WORKLOADS = {
+    # the 270M flavor with Lighthouse (norm, L=3, p=4, k=1536) on layers 2-27,
+    # dense causal attention on layers 0, 1, 28, 29; byte-level vocabulary; batch 1 x 32768 tokens.
+    "cfg5": dict(flavor="ablation_270m_lighthouse_topk1536_pool4_lvl3", B=1, S=32768, vocab=256,
+                 layer="cfg5_layer"),
+}
 
 
 def make_inputs(w, torch, device, seed=1234, heads=None):
@@ -154,30 +164,9 @@ def run_gpu(args, pkg, torch):
 
     ms_step = start.elapsed_time(end) / args.steps
     wall_ms_step = (t1 - t0) * 1e3 / args.steps
-    per_op = {}
-    prev = None
-    for name, ev in marks:
-        if name.endswith("_start"):
-            prev = ev
-            continue
-        per_op.setdefault(name, []).append(prev.elapsed_time(ev))
-        prev = ev
-    work = algorithmic_work(w, S_sel)
-    kernels = {}
-    for name, ts in per_op.items():
-        avg_ms = sum(ts) / len(ts)
-        kind, amount = work[name]
-        if kind == "flop":
-            ach, peak, unit = amount / (avg_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
-        else:
-            ach, peak, unit = amount / (avg_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
-        kernels[name] = {"ms": round(avg_ms, 4), "achieved": round(ach, 2), "unit": unit,
-                         "frac": round(ach / peak, 4), "work": amount}
+    kernels = op_stats(marks, algorithmic_work(w, S_sel))
     dom = max(kernels, key=lambda n: kernels[n]["ms"])
-    kd = kernels[dom]
-    roofline = {"kernel": dom, "bound": "mfma" if kd["unit"] == "TFLOP/s" else "hbm",
-                "achieved": kd["achieved"], "peak": BF16_PEAK_TFLOPS if kd["unit"] == "TFLOP/s" else HBM_PEAK_GBS,
-                "unit": kd["unit"], "frac": kd["frac"], "traffic": measured_traffic(args.workload, dom)}
+    roofline = roofline_of(kernels, dom, args.workload)
     tokens_per_s = B * S / (ms_step * 1e-3)
     cfg = {"workload": f"lighthouse_layer_fwd_bwd_{args.workload}", "B": B, "H": H, "D": D, "S": S,
            "num_levels": L, "pooling_factor": p, "topk": k, "scorer": w["scorer"], "S_sel": S_sel,
@@ -190,6 +179,100 @@ def run_gpu(args, pkg, torch):
         "tokens_per_s": tokens_per_s, "ms_step": ms_step, "wall_ms_step": wall_ms_step, "config": cfg,
         "roofline": roofline, "kernels": kernels,
     }
+
+
+def op_stats(marks, work):
+    """Per-op average launch time from (name, event) marks: each op is timed from
+    the previous mark, and a ``*_start`` mark opens a run of consecutive ops."""
+    per_op = {}
+    prev = None
+    for name, ev in marks:
+        if name.endswith("_start"):
+            prev = ev
+            continue
+        per_op.setdefault(name, []).append(prev.elapsed_time(ev))
+        prev = ev
+    kernels = {}
+    for name, ts in per_op.items():
+        avg_ms = sum(ts) / len(ts)
+        kind, amount = work[name]
+        if kind == "flop":
+            ach, peak, unit = amount / (avg_ms * 1e-3) / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
+        else:
+            ach, peak, unit = amount / (avg_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+        kernels[name] = {"ms": round(avg_ms, 4), "achieved": round(ach, 2), "unit": unit,
+                         "frac": round(ach / peak, 4), "work": amount, "launches": len(ts)}
+    return kernels
+
+
+def roofline_of(kernels, dom, workload):
+    kd = kernels[dom]
+    mfma = kd["unit"] == "TFLOP/s"
+    return {"kernel": dom, "bound": "mfma" if mfma else "hbm", "achieved": kd["achieved"],
+            "peak": BF16_PEAK_TFLOPS if mfma else HBM_PEAK_GBS, "unit": kd["unit"], "frac": kd["frac"],
+            "traffic": measured_traffic(workload, dom)}
+
+
+def run_model(args, pkg, torch):
+    """One training step of the Llama3 model per step (MODEL_WORKLOADS)."""
+    import dataclasses
+    m = MODEL_WORKLOADS[args.workload]
+    wl = WORKLOADS[m["layer"]]
+    L3 = pkg.llama3
+    B, S = m["B"], m["S"]
+    margs = dataclasses.replace(L3.llama3_args[m["flavor"]], vocab_size=m["vocab"], lighthouse_strict=wl["strict"])
+    margs.update_from_config(seq_len=S)
+    dev = torch.device("cuda:0")
+    trainer = L3.Trainer(margs, dev, seed=0)
+    g = torch.Generator(device=dev).manual_seed(1234)
+    tok = torch.randint(0, m["vocab"], (B, S + 1), device=dev, generator=g)
+    x, y = tok[:, :-1].contiguous(), tok[:, 1:].contiguous()
+    for _ in range(args.warmup):
+        trainer.step(x, y)
+    torch.cuda.synchronize()
+    marks = []
+
+    def hook(name):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        marks.append((name, ev))
+
+    sel_mod = pkg.lighthouse_selection
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    sel_mod.set_op_hook(hook)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        loss = trainer.step(x, y)
+    end.record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    sel_mod.set_op_hook(None)
+    ms_step = start.elapsed_time(end) / args.steps
+    S_sel = pkg._native.geometry(S, wl["L"], wl["p"], wl["topk"], wl["strict"])[3]
+    work = algorithmic_work(dict(wl, B=B), S_sel)
+    H = margs.n_heads
+    dense_pairs = S * (S + 1) / 2 * B * H
+    work["dense_attn_fwd"] = ("flop", 4 * D * dense_pairs)
+    work["dense_attn_bwd"] = ("flop", 10 * D * dense_pairs)   # dK/dV (4 products) + dQ (1), as in the layer
+    kernels = op_stats(marks, work)
+    for k in kernels.values():
+        k["ms_per_step"] = round(k["ms"] * k["launches"] / args.steps, 3)
+    dom = max(kernels, key=lambda n: kernels[n]["ms_per_step"])
+    native_ms = sum(k["ms_per_step"] for k in kernels.values())
+    n_light = sum(1 for b in trainer.model.layers.values() if b.attention._use_lighthouse)
+    cfg = {"workload": f"llama3_train_step_{args.workload}", "flavor": m["flavor"], "B": B, "S": S,
+           "vocab_size": margs.vocab_size, "dim": margs.dim, "n_layers": margs.n_layers, "n_heads": H,
+           "ffn_hidden": L3.ffn_hidden_dim(margs.hidden_dim, margs.multiple_of, margs.ffn_dim_multiplier),
+           "lighthouse_layers": n_light, "dense_layers": margs.n_layers - n_light,
+           "num_levels": wl["L"], "pooling_factor": wl["p"], "topk": wl["topk"], "S_sel": S_sel,
+           "strict": wl["strict"], "params": L3.num_params(trainer.master),
+           "optimizer": "AdamW fp32 masters, bf16 compute, clip 1.0", "parallelism": "single GPU"}
+    return {"tokens_per_s": B * S / (ms_step * 1e-3), "ms_step": ms_step,
+            "wall_ms_step": (t1 - t0) * 1e3 / args.steps, "config": cfg,
+            "roofline": roofline_of(kernels, dom, args.workload), "kernels": kernels,
+            "native_ms_per_step": round(native_ms, 3), "final_loss": round(loss.item(), 4)}
 
 
 def run_cpu_baseline(args, torch):
@@ -217,7 +300,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS) + sorted(MODEL_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=0, help="heads in the CPU sample (0: 4, or 1 for dilated)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -240,10 +323,12 @@ def main():
         return
     import __graft_entry__ as G
     pkg = G.load_package()
-    r = run_gpu(args, pkg, torch)
-    cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, torch)
+    model = args.workload in MODEL_WORKLOADS
+    r = run_model(args, pkg, torch) if model else run_gpu(args, pkg, torch)
+    # the CPU oracle covers the layer; a CPU training step of the 270M model is not sampled
+    cpu = None if (args.no_cpu_baseline or model) else run_cpu_baseline(args, torch)
     line = {
-        "metric": METRIC,
+        "metric": MODEL_METRIC if model else METRIC,
         "value": round(r["tokens_per_s"], 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -254,14 +339,19 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: seeded N(0,1) bf16 q/k/v [B,S,H,D] and upstream grad [B,H,S,D], resident in HBM"
-                + ("; 5% of key positions x4" if WORKLOADS[args.workload].get("heavy_keys") else ""),
+        "data": ("synthetic: uniform random token ids [B, S+1] (inputs and shifted labels), random-init weights"
+                 if model else
+                 "synthetic: seeded N(0,1) bf16 q/k/v [B,S,H,D] and upstream grad [B,H,S,D], resident in HBM"
+                 + ("; 5% of key positions x4" if WORKLOADS[args.workload].get("heavy_keys") else "")),
         "config": r["config"],
         "roofline": r["roofline"],
         "cpu_baseline": cpu,
         "kernels": r["kernels"],
         "wall_ms_per_step": round(r["wall_ms_step"], 4),
     }
+    for key in ("native_ms_per_step", "final_loss"):
+        if key in r:
+            line[key] = r[key]
     print(json.dumps(line))
 
 

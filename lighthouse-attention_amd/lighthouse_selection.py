@@ -104,7 +104,9 @@ def set_op_hook(fn):
     layer is enqueued (names: ``pyramid``, ``dilated_scores``, ``select``,
     ``attn_fwd``, ``scatter_fwd``, ``scatter_bwd``, ``attn_bwd_dkdv``,
     ``attn_bwd_dq``, ``pyramid_bwd``) and with ``fwd_start`` / ``bwd_start``
-    before the first one; e.g. to record a stream event per op.  ``None`` removes it."""
+    before the first one; e.g. to record a stream event per op.  The dense causal
+    layers report ``dense_attn_fwd`` / ``dense_attn_bwd`` after ``dense_fwd_start`` /
+    ``dense_bwd_start``.  ``None`` removes it."""
     global _op_hook
     _op_hook = fn
 
