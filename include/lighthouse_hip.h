@@ -191,6 +191,57 @@ int lh_pyramid_bwd(const void *gq, const void *gk, const void *gv,
                    void *dxq, void *dxk, void *dxv,
                    int B, int S, int H, int D, int L, int p, void *stream);
 
+/*
+ * Transformer-block kernels of the Llama3 model that hosts the layer
+ * (lighthouse-attention.patch:583-769 over torchtitan's llama3 model, which
+ * is upstream and not vendored).  They replace torch op chains, not reference
+ * kernels; each names the chain it replaces.
+ */
+
+/*
+ * Rotary embedding fused with the q/k/v split of the projection output.
+ * Replaces apply_rotary_emb (torchtitan llama3 model: view_as_complex * freqs_cis,
+ * fp32, cast back) on wq(x), wk(x) plus the split of wv(x) (patch :707-724).
+ *   x        bf16 rows [B*S] of (Hq + 2 Hkv) * D elements, row stride xs, laid out
+ *            [q heads | k heads | v heads]
+ *   freqs    fp32 [>= S, D/2, 2] (cos, sin) of position t and pair j
+ *   q, k, v  bf16 [B, S, Hq|Hkv, D] contiguous; q and k rotated, v copied
+ */
+int lh_rope_qkv_fwd(const void *x, int64_t xs, const float *freqs, void *q, void *k, void *v,
+                    int B, int S, int Hq, int Hkv, int D, void *stream);
+
+/*
+ * Adjoint: dx = [R(-angle) dq | R(-angle) dk | dv] in the projection-output layout.
+ *   strides  9 int64: (batch, seq, head) element strides of dq, dk, dv (D contiguous)
+ */
+int lh_rope_qkv_bwd(const void *dq, const void *dk, const void *dv, const int64_t *strides,
+                    const float *freqs, void *dx, int64_t xs, int B, int S, int Hq, int Hkv, int D,
+                    void *stream);
+
+/*
+ * RMSNorm over rows of dim elements (dim a multiple of 8, <= 4096):
+ * y = bf16((x * r) * w), r = 1/sqrt(mean(x^2) + eps), rstd[row] = r.
+ * Replaces nn.RMSNorm (torch.rms_norm) of the block's attention_norm, ffn_norm and norm.
+ */
+int lh_rmsnorm_fwd(const void *x, const void *w, void *y, float *rstd, int64_t rows, int dim, float eps,
+                   void *stream);
+
+/*
+ * RMSNorm backward: dx = r g - x r^3 mean(g x) with g = dy w; dw = sum_rows dy x r.
+ * dw_part is caller workspace, fp32 [parts, dim]; dw is bf16 [dim].
+ */
+int lh_rmsnorm_bwd(const void *dy, const void *x, const void *w, const float *rstd, void *dx, void *dw,
+                   float *dw_part, int parts, int64_t rows, int dim, void *stream);
+
+/*
+ * SwiGLU on the fused [h1 | h3] projection (rows of 2F): a = bf16(bf16(silu(h1)) h3).
+ * Replaces F.silu(w1(x)) * w3(x) of FeedForward (torchtitan llama3 model).
+ */
+int lh_swiglu_fwd(const void *h, void *a, int64_t rows, int F, void *stream);
+
+/* SwiGLU backward into the fused layout: dh = [dh1 | dh3] (rows of 2F). */
+int lh_swiglu_bwd(const void *da, const void *h, void *dh, int64_t rows, int F, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,6 +9,6 @@ together with ``_native.py`` and ``liblighthouse_hip.so``.
 from . import _native
 from .lighthouse_selection import *  # noqa: F401,F403
 from .lighthouse_selection import __all__ as _api
-from . import dense_attention, llama3  # noqa: E402  (dense causal layers; the Llama3 model)
+from . import block_ops, dense_attention, llama3  # noqa: E402  (model kernels, dense layers, Llama3)
 
-__all__ = list(_api) + ["_native", "dense_attention", "llama3"]
+__all__ = list(_api) + ["_native", "block_ops", "dense_attention", "llama3"]

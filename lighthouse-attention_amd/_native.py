@@ -52,6 +52,12 @@ _SIGS = {
     "lh_scatter_fwd": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_scatter_bwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_pyramid_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_rope_qkv_fwd": (_I, [_P, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "lh_rope_qkv_bwd": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P]),
+    "lh_rmsnorm_fwd": (_I, [_P, _P, _P, _P, _L, _I, _F, _P]),
+    "lh_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _P]),
+    "lh_swiglu_fwd": (_I, [_P, _P, _L, _I, _P]),
+    "lh_swiglu_bwd": (_I, [_P, _P, _P, _L, _I, _P]),
 }
 EXPORTED = tuple(_SIGS)
 
@@ -342,3 +348,107 @@ def pyramid_bwd(gq, gk, gv, inverse, B: int, S: int, H: int, L: int, p: int, D: 
                                   _ptr(outs[0]), _ptr(outs[1]), _ptr(outs[2]), B, S, H, D, L, p, _stream(dev))
     _check(rc, "lh_pyramid_bwd")
     return tuple(outs)
+
+
+# ---------------------------------------------------------------------------
+# transformer-block ops (rotary embedding, RMSNorm, SwiGLU)
+# ---------------------------------------------------------------------------
+def rope_qkv_fwd(x, freqs, Hq: int, Hkv: int, D: int = D_SUPPORTED):
+    """Split the fused projection output ``x`` [B, S, (Hq+2Hkv)*D] (row stride may
+    exceed the width; D contiguous) into q, k, v [B, S, H, D] contiguous, with q and
+    k rotated by ``freqs`` (fp32 [>=S, D/2, 2] = cos, sin)."""
+    _need_gpu(x, freqs)
+    B, S, W = x.shape
+    assert x.stride(2) == 1 and x.stride(0) == S * x.stride(1), "rows of x must be evenly strided"
+    assert W == (Hq + 2 * Hkv) * D, "x must hold [q | k | v] heads"
+    assert freqs.dtype == torch.float32 and freqs.is_contiguous() and tuple(freqs.shape[1:]) == (D // 2, 2) \
+        and freqs.shape[0] >= S, "freqs must be fp32 [>= S, D/2, 2] contiguous"
+    dev = x.device
+    q = torch.empty(B, S, Hq, D, dtype=torch.bfloat16, device=dev)
+    k = torch.empty(B, S, Hkv, D, dtype=torch.bfloat16, device=dev)
+    v = torch.empty(B, S, Hkv, D, dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib().lh_rope_qkv_fwd(_ptr(x), x.stride(1), _ptr(freqs), _ptr(q), _ptr(k), _ptr(v), B, S, Hq, Hkv, D,
+                                   _stream(dev))
+    _check(rc, "lh_rope_qkv_fwd")
+    return q, k, v
+
+
+def rope_qkv_bwd(dq, dk, dv, freqs, Hq: int, Hkv: int, D: int = D_SUPPORTED):
+    """Adjoint of ``rope_qkv_fwd``: grads of q, k, v ([B, S, H, D], any strides with D
+    contiguous) -> grad of the fused projection output [B, S, (Hq+2Hkv)*D]."""
+    _need_gpu(dq, dk, dv, freqs)
+    B, S = dq.shape[:2]
+    assert tuple(dq.shape) == (B, S, Hq, D) and tuple(dk.shape) == (B, S, Hkv, D) == tuple(dv.shape)
+    assert freqs.dtype == torch.float32 and freqs.is_contiguous() and tuple(freqs.shape[1:]) == (D // 2, 2) \
+        and freqs.shape[0] >= S, "freqs must be fp32 [>= S, D/2, 2] contiguous"
+    dev = dq.device
+    dx = torch.empty(B, S, (Hq + 2 * Hkv) * D, dtype=torch.bfloat16, device=dev)
+    st = (ctypes.c_int64 * 9)(*[int(s) for g in (dq, dk, dv) for s in g.stride()[:3]])
+    for g in (dq, dk, dv):
+        assert g.stride(3) == 1, "head dimension must be contiguous"
+    with torch.cuda.device(dev):
+        rc = lib().lh_rope_qkv_bwd(_ptr(dq), _ptr(dk), _ptr(dv), ctypes.cast(st, _P), _ptr(freqs), _ptr(dx),
+                                   dx.stride(1), B, S, Hq, Hkv, D, _stream(dev))
+    _check(rc, "lh_rope_qkv_bwd")
+    return dx
+
+
+def rmsnorm_fwd(x, w, eps: float):
+    """``y = (x * rsqrt(mean(x^2) + eps)) * w`` over the last dim; returns (y, rstd fp32)."""
+    _need_gpu(x, w)
+    x = x.contiguous()
+    dim = x.shape[-1]
+    assert w.shape == (dim,) and w.is_contiguous(), "weight must be [dim]"
+    rows = x.numel() // dim
+    y = torch.empty_like(x)
+    rstd = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib().lh_rmsnorm_fwd(_ptr(x), _ptr(w), _ptr(y), _ptr(rstd), rows, dim, float(eps), _stream(x.device))
+    _check(rc, "lh_rmsnorm_fwd")
+    return y, rstd
+
+
+RMSNORM_BWD_PARTS = 512
+
+
+def rmsnorm_bwd(dy, x, w, rstd):
+    """Grads of RMSNorm: ``(dx bf16 like x, dw bf16 like w)``."""
+    _need_gpu(dy, x, w, rstd)
+    dy = dy.contiguous()
+    dim = x.shape[-1]
+    rows = x.numel() // dim
+    dx = torch.empty_like(x)
+    dw = torch.empty_like(w)
+    parts = min(RMSNORM_BWD_PARTS, rows)
+    part = torch.empty(parts, dim, dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib().lh_rmsnorm_bwd(_ptr(dy), _ptr(x), _ptr(w), _ptr(rstd), _ptr(dx), _ptr(dw), _ptr(part), parts,
+                                  rows, dim, _stream(x.device))
+    _check(rc, "lh_rmsnorm_bwd")
+    return dx, dw
+
+
+def swiglu_fwd(h):
+    """``h`` [..., 2F] = [h1 | h3] -> ``silu(h1) * h3`` [..., F] (torch's roundings)."""
+    _need_gpu(h)
+    h = h.contiguous()
+    F2 = h.shape[-1]
+    rows = h.numel() // F2
+    a = torch.empty(*h.shape[:-1], F2 // 2, dtype=torch.bfloat16, device=h.device)
+    with torch.cuda.device(h.device):
+        rc = lib().lh_swiglu_fwd(_ptr(h), _ptr(a), rows, F2 // 2, _stream(h.device))
+    _check(rc, "lh_swiglu_fwd")
+    return a
+
+
+def swiglu_bwd(da, h):
+    _need_gpu(da, h)
+    da = da.contiguous()
+    F2 = h.shape[-1]
+    rows = h.numel() // F2
+    dh = torch.empty_like(h)
+    with torch.cuda.device(h.device):
+        rc = lib().lh_swiglu_bwd(_ptr(da), _ptr(h), _ptr(dh), rows, F2 // 2, _stream(h.device))
+    _check(rc, "lh_swiglu_bwd")
+    return dh

@@ -1,0 +1,148 @@
+"""Autograd ops of the Llama3 block around the attention, on the native kernels.
+
+Each op replaces a torch chain of torchtitan's llama3 model (upstream, not
+vendored with the reference; its wiring is ``lighthouse-attention.patch:583-769``):
+
+- ``linear``: ``F.linear`` with a weight gradient split along the token axis
+  (fp32 partial products summed, then rounded once), so the long-K weight
+  gradients of a 32K-token step fill the GPU.
+- ``rope_qkv``: ``apply_rotary_emb`` on ``wq(x)``, ``wk(x)`` plus the split of
+  ``wv(x)``, from one fused ``[q | k | v]`` projection output.
+- ``rms_norm``: ``nn.RMSNorm``.
+- ``swiglu``: ``F.silu(w1(x)) * w3(x)`` from one fused ``[h1 | h3]`` projection.
+
+There is no CPU path: every op raises without the GPU library.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _native as N
+
+__all__ = ["linear", "rope_qkv", "rms_norm", "swiglu", "RMSNorm", "wgrad_splits"]
+
+
+def wgrad_splits(T: int, O: int, I: int, cus: int = 256) -> int:
+    """Number of token slices for the weight gradient ``dy^T x`` ([O, I], K = T):
+    enough 256x256 output tiles times slices to cover the CUs, slices of >= 2048
+    tokens, at most 16."""
+    tiles = -(-O // 256) * -(-I // 256)
+    s = 1
+    while tiles * s < cus and s < 16 and T % (2 * s) == 0 and T // (2 * s) >= 2048:
+        s *= 2
+    return s
+
+
+def _wgrad(dy2, x2):
+    T, O = dy2.shape
+    I = x2.shape[1]
+    s = wgrad_splits(T, O, I)
+    if s == 1:
+        return dy2.t() @ x2
+    part = torch.bmm(dy2.view(s, T // s, O).transpose(1, 2), x2.view(s, T // s, I), out_dtype=torch.float32)
+    return part.sum(0).to(dy2.dtype)
+
+
+class _LinearFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w):
+        ctx.save_for_backward(x, w)
+        return F.linear(x, w)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dy2 = dy.reshape(-1, dy.shape[-1])
+        dx = (dy2 @ w).view(x.shape) if ctx.needs_input_grad[0] else None
+        dw = _wgrad(dy2, x.reshape(-1, x.shape[-1])) if ctx.needs_input_grad[1] else None
+        return dx, dw
+
+
+def _need_bf16(*ts):
+    for t in ts:
+        if not t.is_cuda:
+            raise N.LighthouseHipError("block ops need GPU tensors (no CPU path)")
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"block ops compute in bfloat16; got {t.dtype}")
+
+
+def linear(x, w):
+    """``x @ w^T`` (bf16, no bias)."""
+    _need_bf16(x, w)
+    return _LinearFn.apply(x, w)
+
+
+class _RopeQKVFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, freqs, Hq, Hkv, D):
+        ctx.save_for_backward(freqs)
+        ctx.geo = (Hq, Hkv, D)
+        return N.rope_qkv_fwd(x, freqs, Hq, Hkv, D)
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        (freqs,) = ctx.saved_tensors
+        Hq, Hkv, D = ctx.geo
+        ref = next(g for g in (dq, dk, dv) if g is not None)
+        B, S = ref.shape[:2]
+
+        def z(g, h):
+            if g is None:
+                return torch.zeros(B, S, h, D, dtype=torch.bfloat16, device=ref.device)
+            return g if g.stride(3) == 1 else g.contiguous()
+
+        return N.rope_qkv_bwd(z(dq, Hq), z(dk, Hkv), z(dv, Hkv), freqs, Hq, Hkv, D), None, None, None, None
+
+
+def rope_qkv(x, freqs, Hq: int, Hkv: int, D: int):
+    """Fused projection output ``x`` [B, S, (Hq+2Hkv)*D] -> rotated q, rotated k, v,
+    each [B, S, H, D] contiguous.  ``freqs``: fp32 [>=S, D/2, 2] (cos, sin), e.g.
+    ``torch.view_as_real(freqs_cis)``."""
+    _need_bf16(x)
+    return _RopeQKVFn.apply(x, freqs, Hq, Hkv, D)
+
+
+class _RMSNormFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, eps):
+        y, rstd = N.rmsnorm_fwd(x, w, eps)
+        ctx.save_for_backward(x, w, rstd)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w, rstd = ctx.saved_tensors
+        dx, dw = N.rmsnorm_bwd(dy, x, w, rstd)
+        return dx, dw, None
+
+
+def rms_norm(x, w, eps: float):
+    _need_bf16(x, w)
+    return _RMSNormFn.apply(x, w, eps)
+
+
+class RMSNorm(nn.RMSNorm):
+    """``nn.RMSNorm`` (same parameters and state dict) running the native kernels."""
+
+    def forward(self, x):
+        return rms_norm(x, self.weight, self.eps if self.eps is not None else torch.finfo(x.dtype).eps)
+
+
+class _SwiGLUFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, h):
+        ctx.save_for_backward(h)
+        return N.swiglu_fwd(h)
+
+    @staticmethod
+    def backward(ctx, da):
+        (h,) = ctx.saved_tensors
+        return N.swiglu_bwd(da, h)
+
+
+def swiglu(h):
+    """``[h1 | h3]`` (last dim 2F) -> ``silu(h1) * h3``."""
+    _need_bf16(h)
+    return _SwiGLUFn.apply(h)

@@ -1,0 +1,372 @@
+// Element-wise and row-wise kernels of the Llama3 block around the attention:
+// rotary embedding fused with the q/k/v split of the projection output,
+// RMSNorm forward/backward, SwiGLU forward/backward.  All are HBM-bound
+// streaming passes: one 16-byte vector (8 bf16) per lane and access, every
+// row read once; fp32 arithmetic, one rounding to bf16 per output.
+#include "lh_common.h"
+
+namespace {
+
+constexpr int kVec = 8;  // bf16 per 16-byte access
+
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// rotary embedding on interleaved pairs (x[2j], x[2j+1]) by angle t * f_j:
+//   forward  (a, b) -> (a c - b s, a s + b c)
+//   backward (a, b) -> (a c + b s, b c - a s)      (rotation by -angle)
+// cos/sin come from the caller's table fs[t][j] = (cos, sin), fp32.
+// ---------------------------------------------------------------------------
+struct RopeArgs {
+  const bf16_t* x;       // fwd: projection output rows; bwd: unused
+  const bf16_t* g[3];    // bwd: grads of q, k, v
+  bf16_t* out[3];        // fwd: q, k, v contiguous [B, S, H, D]
+  bf16_t* dx;            // bwd: projection-output grads
+  const float* fs;       // [S, D/2, 2]
+  int64_t xs;            // row stride of x / dx (elements)
+  int64_t gsb[3], gss[3], gsh[3];  // bwd: strides of the three grads
+  int S, Hq, Hkv, D;
+  int64_t rows;          // B * S
+  int chunks;            // 16-byte chunks per row = (Hq + 2 Hkv) * D / 8
+};
+
+template <bool FWD>
+__global__ __launch_bounds__(256) void rope_qkv_kernel(const RopeArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.rows * a.chunks) return;
+  const int64_t row = i / a.chunks;
+  const int c = (int)(i - row * a.chunks);
+  const int col = c * kVec;                 // element column inside the row
+  const int head = col / a.D, d0 = col - head * a.D;
+  const int which = head < a.Hq ? 0 : (head < a.Hq + a.Hkv ? 1 : 2);
+  const int h = which == 0 ? head : (which == 1 ? head - a.Hq : head - a.Hq - a.Hkv);
+  const int nh = which == 0 ? a.Hq : a.Hkv;
+  const int b = (int)(row / a.S), t = (int)(row - (int64_t)b * a.S);
+  uint4 in;
+  if (FWD) {
+    in = ld16(a.x + row * a.xs + col);
+  } else {
+    in = ld16(a.g[which] + b * a.gsb[which] + (int64_t)t * a.gss[which] + (int64_t)h * a.gsh[which] + d0);
+  }
+  uint4 o = in;
+  if (which < 2) {
+    float f[kVec];
+    unpack8(in, f);
+    const float4* cs = reinterpret_cast<const float4*>(a.fs + ((int64_t)t * (a.D / 2) + d0 / 2) * 2);
+    const float4 c01 = cs[0], c23 = cs[1];  // (cos, sin) of pairs j..j+3
+    const float cj[4] = {c01.x, c01.z, c23.x, c23.z};
+    const float sj[4] = {c01.y, c01.w, c23.y, c23.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float x0 = f[2 * j], x1 = f[2 * j + 1];
+      if (FWD) {
+        f[2 * j] = x0 * cj[j] - x1 * sj[j];
+        f[2 * j + 1] = x0 * sj[j] + x1 * cj[j];
+      } else {
+        f[2 * j] = x0 * cj[j] + x1 * sj[j];
+        f[2 * j + 1] = x1 * cj[j] - x0 * sj[j];
+      }
+    }
+    o = pack8(f);
+  }
+  if (FWD) {
+    st16(a.out[which] + ((row * nh + h) * a.D + d0), o);
+  } else {
+    st16(a.dx + row * a.xs + col, o);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm: y = bf16((x * r) * w), r = 1 / sqrt(mean(x^2) + eps), fp32 inside.
+// One wave per row; each lane holds up to 8 16-byte chunks (dim <= 4096, dim % 8 == 0).
+// ---------------------------------------------------------------------------
+constexpr int kMaxChunksPerLane = 8;  // dim <= 64 * 8 * 8 = 4096
+
+template <int NC>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
+                                                          bf16_t* __restrict__ y, float* __restrict__ rstd,
+                                                          int64_t rows, int dim, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const bf16_t* xr = x + row * dim;
+  float v[NC][kVec];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int col = (c * 64 + lane) * kVec;
+    unpack8(col < dim ? ld16(xr + col) : make_uint4(0, 0, 0, 0), v[c]);
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) ss += v[c][e] * v[c][e];
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / (float)dim + eps);
+  if (lane == 0) rstd[row] = r;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int col = (c * 64 + lane) * kVec;
+    if (col < dim) {
+      float wf[kVec];
+      unpack8(ld16(w + col), wf);
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) v[c][e] = (v[c][e] * r) * wf[e];
+      st16(y + row * dim + col, pack8(v[c]));
+    }
+  }
+}
+
+// dx = r * g - x * r^3 * mean(g * x), g = dy * w;  dw = sum over rows of dy * x * r.
+// Block = 4 waves over a contiguous range of rows; each block leaves one fp32
+// partial row of dw, reduced by rmsnorm_dw_kernel.
+template <int NC>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const bf16_t* __restrict__ dy, const bf16_t* __restrict__ x,
+                                                          const bf16_t* __restrict__ w, const float* __restrict__ rstd,
+                                                          bf16_t* __restrict__ dx, float* __restrict__ dw_part,
+                                                          int64_t rows, int dim, int64_t rows_per_block) {
+  // waves 1..3 hand their dw partials to wave 0, half of the lane's chunks at a time
+  __shared__ float red[3][64 * kVec * kMaxChunksPerLane / 2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t r1 = min(rows, r0 + rows_per_block);
+  float wf[NC][kVec], acc[NC][kVec];
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int col = (c * 64 + lane) * kVec;
+    unpack8(col < dim ? ld16(w + col) : zero, wf[c]);
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) acc[c][e] = 0.f;
+  }
+  for (int64_t row = r0 + wave; row < r1; row += 4) {
+    float g[NC][kVec], xv[NC][kVec], d[NC][kVec];
+    float dot = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int col = (c * 64 + lane) * kVec;
+      unpack8(col < dim ? ld16(dy + row * dim + col) : zero, d[c]);
+      unpack8(col < dim ? ld16(x + row * dim + col) : zero, xv[c]);
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) {
+        g[c][e] = d[c][e] * wf[c][e];
+        dot += g[c][e] * xv[c][e];
+      }
+    }
+    dot = wave_sum(dot);
+    const float r = rstd[row];
+    const float k3 = r * r * r * dot / (float)dim;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) {
+        acc[c][e] += d[c][e] * (xv[c][e] * r);
+        g[c][e] = r * g[c][e] - xv[c][e] * k3;
+      }
+      const int col = (c * 64 + lane) * kVec;
+      if (col < dim) st16(dx + row * dim + col, pack8(g[c]));
+    }
+  }
+  // reduce the four waves' dw partials through LDS, NC chunks at a time in halves
+  float* red0 = &red[0][0];
+  constexpr int HALF = (NC + 1) / 2;
+#pragma unroll
+  for (int part = 0; part < 2; ++part) {
+    const int cb = part * HALF, ce = min(NC, cb + HALF);
+    if (wave > 0) {
+      for (int c = cb; c < ce; ++c)
+#pragma unroll
+        for (int e = 0; e < kVec; ++e)
+          red0[(wave - 1) * (64 * kVec * kMaxChunksPerLane / 2) + ((c - cb) * 64 + lane) * kVec + e] = acc[c][e];
+    }
+    __syncthreads();
+    if (wave == 0) {
+      for (int c = cb; c < ce; ++c) {
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) {
+          float s = acc[c][e];
+#pragma unroll
+          for (int q = 0; q < 3; ++q) s += red0[q * (64 * kVec * kMaxChunksPerLane / 2) + ((c - cb) * 64 + lane) * kVec + e];
+          if ((c * 64 + lane) * kVec < dim) dw_part[(int64_t)blockIdx.x * dim + (c * 64 + lane) * kVec + e] = s;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// dw[i] = sum over partial rows; a block owns 64 columns, its 4 waves split the rows.
+__global__ __launch_bounds__(256) void rmsnorm_dw_kernel(const float* __restrict__ part, bf16_t* __restrict__ dw,
+                                                         int parts, int dim) {
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i = blockIdx.x * 64 + lane;
+  float s = 0.f;
+  if (i < dim)
+    for (int p = wave; p < parts; p += 4) s += part[(int64_t)p * dim + i];
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && i < dim) dw[i] = f32_to_bf16(red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane]);
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU on the fused [h1 | h3] projection output (row length 2F):
+//   a = bf16(bf16(silu(h1)) * h3)
+//   backward: dh3 = bf16(da * bf16(silu(h1))),
+//             dh1 = bf16(bf16(da * h3) * sigmoid(h1) * (1 + h1 (1 - sigmoid(h1))))
+// (the roundings of torch's separate silu and mul ops, in the same order).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+template <bool FWD>
+__global__ __launch_bounds__(256) void swiglu_kernel(const bf16_t* __restrict__ h, const bf16_t* __restrict__ da,
+                                                     bf16_t* __restrict__ out, int64_t rows, int F) {
+  const int cpr = F / kVec;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * cpr) return;
+  const int64_t row = i / cpr;
+  const int col = (int)(i - row * cpr) * kVec;
+  float h1[kVec], h3[kVec];
+  unpack8(ld16(h + row * 2 * F + col), h1);
+  unpack8(ld16(h + row * 2 * F + F + col), h3);
+  if (FWD) {
+    float a[kVec];
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) {
+      const float s = bf16_round(h1[e] / (1.0f + expf(-h1[e])));
+      a[e] = s * h3[e];
+    }
+    st16(out + row * F + col, pack8(a));
+  } else {
+    float g[kVec], d1[kVec], d3[kVec];
+    unpack8(ld16(da + row * F + col), g);
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) {
+      const float sg = 1.0f / (1.0f + expf(-h1[e]));
+      const float s = bf16_round(h1[e] / (1.0f + expf(-h1[e])));
+      d3[e] = g[e] * s;
+      const float gs = bf16_round(g[e] * h3[e]);
+      d1[e] = gs * sg * (1.0f + h1[e] * (1.0f - sg));
+    }
+    st16(out + row * 2 * F + col, pack8(d1));
+    st16(out + row * 2 * F + F + col, pack8(d3));
+  }
+}
+
+inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+inline int grid_of(int64_t n) { return (int)((n + 255) / 256); }
+
+}  // namespace
+
+extern "C" int lh_rope_qkv_fwd(const void* x, int64_t xs, const float* freqs, void* q, void* k, void* v,
+                               int B, int S, int Hq, int Hkv, int D, void* stream) {
+  if (!x || !freqs || !q || !k || !v || B <= 0 || S <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0) return LH_ERR_INVALID_ARG;
+  if (D % 8 || xs < (int64_t)(Hq + 2 * Hkv) * D || xs % 8 || !al16(x) || !al16(q) || !al16(k) || !al16(v) ||
+      !al16(freqs))
+    return LH_ERR_INVALID_ARG;
+  RopeArgs a{};
+  a.x = (const bf16_t*)x;
+  a.out[0] = (bf16_t*)q; a.out[1] = (bf16_t*)k; a.out[2] = (bf16_t*)v;
+  a.fs = freqs; a.xs = xs; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = D;
+  a.rows = (int64_t)B * S;
+  a.chunks = (Hq + 2 * Hkv) * D / kVec;
+  const int64_t n = a.rows * a.chunks;
+  if (n / 256 + 1 > 0x7fffffffLL) return LH_ERR_UNSUPPORTED;
+  rope_qkv_kernel<true><<<grid_of(n), 256, 0, (hipStream_t)stream>>>(a);
+  LH_CHECK_LAUNCH();
+  return LH_OK;
+}
+
+extern "C" int lh_rope_qkv_bwd(const void* dq, const void* dk, const void* dv, const int64_t* strides,
+                               const float* freqs, void* dx, int64_t xs, int B, int S, int Hq, int Hkv, int D,
+                               void* stream) {
+  if (!dq || !dk || !dv || !strides || !freqs || !dx || B <= 0 || S <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0)
+    return LH_ERR_INVALID_ARG;
+  if (D % 8 || xs < (int64_t)(Hq + 2 * Hkv) * D || xs % 8 || !al16(dq) || !al16(dk) || !al16(dv) || !al16(dx) ||
+      !al16(freqs))
+    return LH_ERR_INVALID_ARG;
+  RopeArgs a{};
+  a.g[0] = (const bf16_t*)dq; a.g[1] = (const bf16_t*)dk; a.g[2] = (const bf16_t*)dv;
+  for (int i = 0; i < 3; ++i) {
+    a.gsb[i] = strides[3 * i]; a.gss[i] = strides[3 * i + 1]; a.gsh[i] = strides[3 * i + 2];
+    if ((a.gsb[i] | a.gss[i] | a.gsh[i]) % 8) return LH_ERR_INVALID_ARG;
+  }
+  a.dx = (bf16_t*)dx; a.fs = freqs; a.xs = xs; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = D;
+  a.rows = (int64_t)B * S;
+  a.chunks = (Hq + 2 * Hkv) * D / kVec;
+  const int64_t n = a.rows * a.chunks;
+  if (n / 256 + 1 > 0x7fffffffLL) return LH_ERR_UNSUPPORTED;
+  rope_qkv_kernel<false><<<grid_of(n), 256, 0, (hipStream_t)stream>>>(a);
+  LH_CHECK_LAUNCH();
+  return LH_OK;
+}
+
+#define LH_NC_DISPATCH(NCV, CALL) \
+  switch (NCV) {                  \
+    case 1: { constexpr int NC = 1; CALL; break; } \
+    case 2: { constexpr int NC = 2; CALL; break; } \
+    case 3: { constexpr int NC = 3; CALL; break; } \
+    case 4: { constexpr int NC = 4; CALL; break; } \
+    case 5: { constexpr int NC = 5; CALL; break; } \
+    case 6: { constexpr int NC = 6; CALL; break; } \
+    case 7: { constexpr int NC = 7; CALL; break; } \
+    case 8: { constexpr int NC = 8; CALL; break; } \
+    default: return LH_ERR_UNSUPPORTED;            \
+  }
+
+extern "C" int lh_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int64_t rows, int dim, float eps,
+                              void* stream) {
+  if (!x || !w || !y || !rstd || rows <= 0 || dim <= 0 || !(eps >= 0.f)) return LH_ERR_INVALID_ARG;
+  if (!al16(x) || !al16(w) || !al16(y)) return LH_ERR_INVALID_ARG;
+  if (dim % 8 || dim > 4096) return LH_ERR_UNSUPPORTED;  // whole 16-byte chunks, <= 8 per lane
+  const int nc = (dim + 511) / 512;
+  const int grid = (int)((rows + 3) / 4);
+  LH_NC_DISPATCH(nc, (rmsnorm_fwd_kernel<NC><<<grid, 256, 0, (hipStream_t)stream>>>(
+                          (const bf16_t*)x, (const bf16_t*)w, (bf16_t*)y, rstd, rows, dim, eps)));
+  LH_CHECK_LAUNCH();
+  return LH_OK;
+}
+
+extern "C" int lh_rmsnorm_bwd(const void* dy, const void* x, const void* w, const float* rstd, void* dx, void* dw,
+                              float* dw_part, int parts, int64_t rows, int dim, void* stream) {
+  if (!dy || !x || !w || !rstd || !dx || !dw || !dw_part || rows <= 0 || dim <= 0 || parts <= 0)
+    return LH_ERR_INVALID_ARG;
+  if (!al16(dy) || !al16(x) || !al16(w) || !al16(dx)) return LH_ERR_INVALID_ARG;
+  if (dim % 8 || dim > 4096) return LH_ERR_UNSUPPORTED;
+  const int nc = (dim + 511) / 512;
+  const int64_t rpb = (rows + parts - 1) / parts;
+  const int used = (int)((rows + rpb - 1) / rpb);  // blocks that own at least one row
+  LH_NC_DISPATCH(nc, (rmsnorm_bwd_kernel<NC><<<used, 256, 0, (hipStream_t)stream>>>(
+                          (const bf16_t*)dy, (const bf16_t*)x, (const bf16_t*)w, rstd, (bf16_t*)dx, dw_part,
+                          rows, dim, rpb)));
+  LH_CHECK_LAUNCH();
+  rmsnorm_dw_kernel<<<(dim + 63) / 64, 256, 0, (hipStream_t)stream>>>(dw_part, (bf16_t*)dw, used, dim);
+  LH_CHECK_LAUNCH();
+  return LH_OK;
+}
+
+extern "C" int lh_swiglu_fwd(const void* h, void* a, int64_t rows, int F, void* stream) {
+  if (!h || !a || rows <= 0 || F <= 0 || F % 8 || !al16(h) || !al16(a)) return LH_ERR_INVALID_ARG;
+  const int64_t n = rows * (F / kVec);
+  if (n / 256 + 1 > 0x7fffffffLL) return LH_ERR_UNSUPPORTED;
+  swiglu_kernel<true><<<grid_of(n), 256, 0, (hipStream_t)stream>>>((const bf16_t*)h, nullptr, (bf16_t*)a, rows, F);
+  LH_CHECK_LAUNCH();
+  return LH_OK;
+}
+
+extern "C" int lh_swiglu_bwd(const void* da, const void* h, void* dh, int64_t rows, int F, void* stream) {
+  if (!da || !h || !dh || rows <= 0 || F <= 0 || F % 8 || !al16(h) || !al16(da) || !al16(dh))
+    return LH_ERR_INVALID_ARG;
+  const int64_t n = rows * (F / kVec);
+  if (n / 256 + 1 > 0x7fffffffLL) return LH_ERR_UNSUPPORTED;
+  swiglu_kernel<false><<<grid_of(n), 256, 0, (hipStream_t)stream>>>((const bf16_t*)h, (const bf16_t*)da, (bf16_t*)dh,
+                                                                     rows, F);
+  LH_CHECK_LAUNCH();
+  return LH_OK;
+}

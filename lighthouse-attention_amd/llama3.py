@@ -5,8 +5,11 @@ This is torchtitan's Llama3 model as the Lighthouse patch wires it
 attention of every layer runs on the gfx950 kernels of this package — the
 Lighthouse layer (``LighthouseLocal``) on the selection layers, the dense
 causal kernel (``ScaledDotProductAttention``) on ``lighthouse_full_attn_layers``
-and on models without selection.  Projections, norms and the SwiGLU MLP are
-plain torch modules (their GEMMs go to hipBLASLt).
+and on models without selection.  The rest of the block runs on this
+package's kernels too (``block_ops``: fused rotary embedding + q/k/v split,
+RMSNorm, SwiGLU); the projections are hipBLASLt GEMMs, fused per input
+(``[wq; wk; wv]``, ``[w1; w3]``) with the parameters kept as torchtitan names
+them, and weight gradients split along the token axis.
 
 torchtitan itself is not vendored with the reference (upstream dependency; the
 patch applies to its ``llama3`` package).  Its unchanged parts are restated
@@ -31,6 +34,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import block_ops as ops
 from .dense_attention import ScaledDotProductAttention
 from .lighthouse_selection import (
     DialatedLighthouseNormScorer,
@@ -278,10 +282,10 @@ class Attention(nn.Module):
 
     def forward(self, x: torch.Tensor, freqs_cis: torch.Tensor, attention_masks=None):
         bs, seqlen, _ = x.shape
-        xq = self.wq(x).view(bs, seqlen, -1, self.head_dim)
-        xk = self.wk(x).view(bs, seqlen, -1, self.head_dim)
-        xv = self.wv(x).view(bs, seqlen, -1, self.head_dim)
-        xq, xk = apply_rotary_emb(xq, xk, freqs_cis)
+        # one projection GEMM for [q | k | v]; rotary embedding and the split in one pass
+        wqkv = torch.cat([self.wq.weight, self.wk.weight, self.wv.weight])
+        xqkv = ops.linear(x, wqkv)
+        xq, xk, xv = ops.rope_qkv(xqkv, torch.view_as_real(freqs_cis), self.n_heads, self.n_kv_heads, self.head_dim)
         if attention_masks is not None:
             raise NotImplementedError("document masks need flex attention, which is not part of this build")
         if self.use_selection_lighthouse and self._use_lighthouse:
@@ -295,7 +299,7 @@ class Attention(nn.Module):
             values = repeat_kv(xv, self.n_rep)
             out = self.inner_attention(xq.transpose(1, 2), keys.transpose(1, 2), values.transpose(1, 2))
         out = out.transpose(1, 2).contiguous().view(bs, seqlen, -1)
-        return self.wo(out)
+        return ops.linear(out, self.wo.weight)
 
 
 def ffn_hidden_dim(hidden_dim: int, multiple_of: int, ffn_dim_multiplier: float | None) -> int:
@@ -319,7 +323,9 @@ class FeedForward(nn.Module):
         self.w3 = nn.Linear(dim, h, bias=False)
 
     def forward(self, x):
-        return self.w2(F.silu(self.w1(x)) * self.w3(x))
+        # [h1 | h3] from one GEMM, then silu(h1) * h3 in one pass
+        h = ops.linear(x, torch.cat([self.w1.weight, self.w3.weight]))
+        return ops.linear(ops.swiglu(h), self.w2.weight)
 
     def init_weights(self, init_std: float):
         nn.init.trunc_normal_(self.w1.weight, mean=0.0, std=0.02)
@@ -335,8 +341,8 @@ class TransformerBlock(nn.Module):
         self.attention = Attention(args)
         ffn_hidden = args.hidden_dim if args.hidden_dim is not None else 4 * args.dim
         self.feed_forward = FeedForward(args.dim, ffn_hidden, args.multiple_of, args.ffn_dim_multiplier)
-        self.attention_norm = nn.RMSNorm(args.dim, eps=args.norm_eps)
-        self.ffn_norm = nn.RMSNorm(args.dim, eps=args.norm_eps)
+        self.attention_norm = ops.RMSNorm(args.dim, eps=args.norm_eps)
+        self.ffn_norm = ops.RMSNorm(args.dim, eps=args.norm_eps)
         if args.depth_init:
             self.weight_init_std = 0.02 / (2 * (layer_id + 1)) ** 0.5
         else:
@@ -374,7 +380,7 @@ class Transformer(nn.Module):
             if key in self.layers:
                 self.layers[key].attention.set_use_lighthouse(False)
                 self._full_attn_layers.add(key)
-        self.norm = nn.RMSNorm(args.dim, eps=args.norm_eps)
+        self.norm = ops.RMSNorm(args.dim, eps=args.norm_eps)
         self.output = nn.Linear(args.dim, args.vocab_size, bias=False)
 
     def _precompute_freqs_cis(self):
@@ -396,7 +402,7 @@ class Transformer(nn.Module):
         h = self.tok_embeddings(tokens)
         for layer in self.layers.values():
             h = layer(h, self.freqs_cis, attention_masks)
-        return self.output(self.norm(h))
+        return ops.linear(self.norm(h), self.output.weight)
 
 
 def cast_params_(model: nn.Module, dtype: torch.dtype) -> nn.Module:

@@ -79,6 +79,19 @@ def test_host_validation_rejects_before_launch(pkg):
                               null) == 1
     assert lib.lh_select_geometry(4096, 3, 4, 1536, 1, None, None, None, None) == 2
     assert lib.lh_select_geometry(4096, 1, 4, 256, 0, None, None, None, None) == 1
+    # transformer-block kernels
+    assert lib.lh_rope_qkv_fwd(null, 3072, null, null, null, null, 1, 16, 8, 8, 128, null) == 1
+    assert lib.lh_rope_qkv_bwd(null, null, null, null, null, null, 3072, 1, 16, 8, 8, 128, null) == 1
+    assert lib.lh_rmsnorm_fwd(null, null, null, null, 16, 1024, ctypes.c_float(1e-5), null) == 1
+    assert lib.lh_rmsnorm_bwd(null, null, null, null, null, null, null, 4, 16, 1024, null) == 1
+    assert lib.lh_swiglu_fwd(null, null, 16, 1024, null) == 1
+    assert lib.lh_swiglu_bwd(null, null, null, 16, 1000, null) == 1
+    # a row too long for one wave's registers is refused as unsupported
+    x = (ctypes.c_uint16 * 1024)()
+    r = (ctypes.c_float * 4)()
+    ptr = ctypes.cast(x, ctypes.c_void_p)
+    assert lib.lh_rmsnorm_fwd(ptr, ptr, ptr, ctypes.cast(r, ctypes.c_void_p), 1, 8192,
+                              ctypes.c_float(1e-5), null) in (1, 4)
 
 
 def test_no_cpu_fallback(pkg):

@@ -73,9 +73,56 @@ def test_model_dense_layers_against_fp32_attention(pkg, dev):
         assert_close(p.grad, pr.grad.float(), name, max_abs=1e-1, rel_l2=3e-2)
 
 
+def _torch_forward(m, tok):
+    """torchtitan's Llama3 forward restated with torch ops in fp32 on the model's
+    (bf16-valued) weights; causal attention from the oracle."""
+    a = m.model_args
+    P = {k: v.float() for k, v in m.state_dict().items() if k != "freqs_cis"}
+    import importlib
+    L = importlib.import_module(type(m).__module__)
+    h = P["tok_embeddings.weight"][tok]
+    S = tok.shape[1]
+    hd = a.dim // a.n_heads
+    for i in range(a.n_layers):
+        p = f"layers.{i}."
+        xn = torch.nn.functional.rms_norm(h, (a.dim,), P[p + "attention_norm.weight"], a.norm_eps)
+        q = (xn @ P[p + "attention.wq.weight"].t()).view(*tok.shape, -1, hd)
+        k = (xn @ P[p + "attention.wk.weight"].t()).view(*tok.shape, -1, hd)
+        v = (xn @ P[p + "attention.wv.weight"].t()).view(*tok.shape, -1, hd)
+        q, k = L.apply_rotary_emb(q, k, m.freqs_cis)
+        o = O.sdpa_causal(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
+        h = h + o.transpose(1, 2).reshape(*tok.shape, -1) @ P[p + "attention.wo.weight"].t()
+        xn = torch.nn.functional.rms_norm(h, (a.dim,), P[p + "ffn_norm.weight"], a.norm_eps)
+        f = torch.nn.functional.silu(xn @ P[p + "feed_forward.w1.weight"].t()) * (xn @ P[p + "feed_forward.w3.weight"].t())
+        h = h + f @ P[p + "feed_forward.w2.weight"].t()
+    h = torch.nn.functional.rms_norm(h, (a.dim,), P["norm.weight"], a.norm_eps)
+    return h @ P["output.weight"].t()
+
+
+def test_model_against_torch_restatement(pkg, dev):
+    """Whole dense model (native RMSNorm, fused projections, RoPE, SwiGLU, attention)
+    against the fp32 torch restatement on the same bf16 weights: logits rel-L2 <= 2e-2,
+    loss within 1e-2."""
+    L = pkg.llama3
+    torch.manual_seed(3)
+    with torch.device(dev):
+        m = L.Transformer(_tiny(pkg, n_layers=2))
+    m.init_weights(dev)
+    L.cast_params_(m, torch.bfloat16)
+    tok = torch.randint(0, 256, (1, 1536), device=dev, generator=torch.Generator(dev).manual_seed(4))
+    with torch.no_grad():
+        out = m(tok).float()
+        ref = _torch_forward(m, tok)
+    assert_close(out, ref, "logits", max_abs=5e-2, rel_l2=2e-2)
+    lbl = tok.roll(-1, 1).flatten()
+    l1 = torch.nn.functional.cross_entropy(out.flatten(0, 1), lbl).item()
+    l2 = torch.nn.functional.cross_entropy(ref.flatten(0, 1), lbl).item()
+    assert abs(l1 - l2) < 1e-2, (l1, l2)
+
+
 def test_lighthouse_layer_wiring_is_exact(pkg, dev):
     """A Lighthouse layer of the model computes wo(lighthouse_layer(rope(wq x), rope(wk x), wv x))."""
-    L = pkg.llama3
+    L, ops = pkg.llama3, pkg.block_ops
     args = _tiny(pkg, use_selection_lighthouse=True, lighthouse_num_levels=2, lighthouse_pooling_factor=4,
                  lighthouse_topk=256, lighthouse_full_attn_layers=[0, 2])
     torch.manual_seed(1)
@@ -86,25 +133,31 @@ def test_lighthouse_layer_wiring_is_exact(pkg, dev):
     att = m.layers["1"].attention
     S = 2048
     x = torch.randn(1, S, 256, device=dev, generator=torch.Generator(dev).manual_seed(2)).bfloat16()
+    fr = torch.view_as_real(m.freqs_cis)
+
+    def qkv(a):
+        # separate projections equal the fused one's column blocks; rope as torchtitan's op
+        q, k, v = a.wq(x).view(1, S, 2, 128), a.wk(x).view(1, S, 2, 128), a.wv(x).view(1, S, 2, 128)
+        fq, fk, fv = ops.rope_qkv(ops.linear(x, torch.cat([a.wq.weight, a.wk.weight, a.wv.weight])), fr, 2, 2, 128)
+        rq, rk = L.apply_rotary_emb(q, k, m.freqs_cis)
+        assert_close(fv, v, "v split", max_abs=1e-2, rel_l2=5e-3)
+        assert_close(fq, rq, "rotated q", max_abs=1e-2, rel_l2=5e-3)
+        assert_close(fk, rk, "rotated k", max_abs=1e-2, rel_l2=5e-3)
+        return fq, fk, fv
+
     with torch.no_grad():
         got = att(x, m.freqs_cis)
-        q = att.wq(x).view(1, S, 2, 128)
-        k = att.wk(x).view(1, S, 2, 128)
-        v = att.wv(x).view(1, S, 2, 128)
-        q, k = L.apply_rotary_emb(q, k, m.freqs_cis)
+        q, k, v = qkv(att)
         o, _ = pkg.lighthouse_layer(q, k, v, 2, 4, 256)
-        want = att.wo(o.transpose(1, 2).reshape(1, S, 256))
+        want = ops.linear(o.transpose(1, 2).reshape(1, S, 256), att.wo.weight)
     assert torch.equal(got, want)
     # the full-attention layers of the same model take the dense kernel
     with torch.no_grad():
-        got0 = m.layers["0"].attention(x, m.freqs_cis)
         a0 = m.layers["0"].attention
-        q = a0.wq(x).view(1, S, 2, 128)
-        k = a0.wk(x).view(1, S, 2, 128)
-        v = a0.wv(x).view(1, S, 2, 128)
-        q, k = L.apply_rotary_emb(q, k, m.freqs_cis)
+        got0 = a0(x, m.freqs_cis)
+        q, k, v = qkv(a0)
         o = pkg.dense_attention.dense_causal_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
-        want0 = a0.wo(o.transpose(1, 2).reshape(1, S, 256))
+        want0 = ops.linear(o.transpose(1, 2).reshape(1, S, 256), a0.wo.weight)
     assert torch.equal(got0, want0)
 
 
