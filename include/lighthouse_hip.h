@@ -228,7 +228,7 @@ int lh_rmsnorm_fwd(const void *x, const void *w, void *y, float *rstd, int64_t r
 
 /*
  * RMSNorm backward: dx = r g - x r^3 mean(g x) with g = dy w; dw = sum_rows dy x r.
- * dw_part is caller workspace, fp32 [parts, dim]; dw is bf16 [dim].
+ * dw_part is caller workspace, fp32 [dim, parts]; dw is bf16 [dim].
  */
 int lh_rmsnorm_bwd(const void *dy, const void *x, const void *w, const float *rstd, void *dx, void *dw,
                    float *dw_part, int parts, int64_t rows, int dim, void *stream);

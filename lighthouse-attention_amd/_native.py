@@ -421,7 +421,7 @@ def rmsnorm_bwd(dy, x, w, rstd):
     dx = torch.empty_like(x)
     dw = torch.empty_like(w)
     parts = min(RMSNORM_BWD_PARTS, rows)
-    part = torch.empty(parts, dim, dtype=torch.float32, device=x.device)
+    part = torch.empty(dim, parts, dtype=torch.float32, device=x.device)
     with torch.cuda.device(x.device):
         rc = lib().lh_rmsnorm_bwd(_ptr(dy), _ptr(x), _ptr(w), _ptr(rstd), _ptr(dx), _ptr(dw), _ptr(part), parts,
                                   rows, dim, _stream(x.device))

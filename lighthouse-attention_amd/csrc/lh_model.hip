@@ -124,7 +124,8 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const bf16_t* __restri
 
 // dx = r * g - x * r^3 * mean(g * x), g = dy * w;  dw = sum over rows of dy * x * r.
 // Block = 4 waves over a contiguous range of rows; each block leaves one fp32
-// partial row of dw, reduced by rmsnorm_dw_kernel.
+// partial of every dw column (stored column-major, [dim][blocks]) for
+// rmsnorm_dw_kernel.
 template <int NC>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const bf16_t* __restrict__ dy, const bf16_t* __restrict__ x,
                                                           const bf16_t* __restrict__ w, const float* __restrict__ rstd,
@@ -192,7 +193,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const bf16_t* __restri
           float s = acc[c][e];
 #pragma unroll
           for (int q = 0; q < 3; ++q) s += red0[q * (64 * kVec * kMaxChunksPerLane / 2) + ((c - cb) * 64 + lane) * kVec + e];
-          if ((c * 64 + lane) * kVec < dim) dw_part[(int64_t)blockIdx.x * dim + (c * 64 + lane) * kVec + e] = s;
+          if ((c * 64 + lane) * kVec < dim) dw_part[(int64_t)((c * 64 + lane) * kVec + e) * gridDim.x + blockIdx.x] = s;
         }
       }
     }
@@ -200,18 +201,18 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const bf16_t* __restri
   }
 }
 
-// dw[i] = sum over partial rows; a block owns 64 columns, its 4 waves split the rows.
+// dw[i] = sum of column i's partials: one wave per column, lanes stride the
+// contiguous partials, then a wave reduction (fixed order: deterministic).
 __global__ __launch_bounds__(256) void rmsnorm_dw_kernel(const float* __restrict__ part, bf16_t* __restrict__ dw,
                                                          int parts, int dim) {
-  __shared__ float red[4][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int i = blockIdx.x * 64 + lane;
+  const int lane = threadIdx.x & 63;
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= dim) return;
+  const float* col = part + (int64_t)i * parts;
   float s = 0.f;
-  if (i < dim)
-    for (int p = wave; p < parts; p += 4) s += part[(int64_t)p * dim + i];
-  red[wave][lane] = s;
-  __syncthreads();
-  if (wave == 0 && i < dim) dw[i] = f32_to_bf16(red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane]);
+  for (int p = lane; p < parts; p += 64) s += col[p];
+  s = wave_sum(s);
+  if (lane == 0) dw[i] = f32_to_bf16(s);
 }
 
 // ---------------------------------------------------------------------------
@@ -346,7 +347,7 @@ extern "C" int lh_rmsnorm_bwd(const void* dy, const void* x, const void* w, cons
                           (const bf16_t*)dy, (const bf16_t*)x, (const bf16_t*)w, rstd, (bf16_t*)dx, dw_part,
                           rows, dim, rpb)));
   LH_CHECK_LAUNCH();
-  rmsnorm_dw_kernel<<<(dim + 63) / 64, 256, 0, (hipStream_t)stream>>>(dw_part, (bf16_t*)dw, used, dim);
+  rmsnorm_dw_kernel<<<(dim + 3) / 4, 256, 0, (hipStream_t)stream>>>(dw_part, (bf16_t*)dw, used, dim);
   LH_CHECK_LAUNCH();
   return LH_OK;
 }
