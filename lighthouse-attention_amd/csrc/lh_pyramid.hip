@@ -116,6 +116,10 @@ struct PyrBwdArgs {
   long long rows;
 };
 
+// One 16-lane group per (b, t, h) row, 8 d each.  All levels' inverse lookups
+// are issued first, then all gradient-row loads, so a row costs two dependent
+// memory round trips instead of two per level.
+template <int NL>
 __global__ __launch_bounds__(256) void pyramid_bwd_kernel(const PyrBwdArgs a) {
   const int tid = threadIdx.x;
   const long long row = (long long)blockIdx.x * 16 + (tid >> 4);
@@ -127,26 +131,36 @@ __global__ __launch_bounds__(256) void pyramid_bwd_kernel(const PyrBwdArgs a) {
   const int b = (int)(bt / a.S);
   const size_t irow = (size_t)(b * a.H + h) * a.S_tot;
   const int64_t gbase = (int64_t)b * a.gb + (int64_t)h * a.gh + 8 * l16;
+  int s[NL];
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+    const int node = t >> (l * a.shift);
+    const int r = a.off[l + 1] + node;
+    s[l] = node < a.len[l + 1] ? (a.inv ? a.inv[irow + r] : r) : -1;
+  }
+  const uint4 z = make_uint4(0, 0, 0, 0);
+  uint4 gq[NL], gk[NL], gv[NL];
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+    const int64_t go = gbase + (int64_t)max(s[l], 0) * a.gs;
+    gq[l] = (a.gq && s[l] >= 0) ? ld16(a.gq + go) : z;
+    gk[l] = (a.gk && s[l] >= 0) ? ld16(a.gk + go) : z;
+    gv[l] = (a.gv && s[l] >= 0) ? ld16(a.gv + go) : z;
+  }
   float fq[8] = {0}, fk[8] = {0}, fv[8] = {0};
-  for (int lvl = 1; lvl <= a.L; ++lvl) {
-    const int cs = (lvl - 1) * a.shift;
-    const int node = t >> cs;
-    if (node >= a.len[lvl]) continue;
-    const int r = a.off[lvl] + node;
-    const int s = a.inv ? a.inv[irow + r] : r;
-    if (s < 0) continue;
-    const float w = 1.0f / (float)(1 << cs);
-    const int64_t go = gbase + (int64_t)s * a.gs;
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+    const float w = 1.0f / (float)(1 << (l * a.shift));
     float g[8];
-    if (a.gq) { unpack8(ld16(a.gq + go), g);
+    unpack8(gq[l], g);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) fq[e] = fmaf(g[e], w, fq[e]); }
-    if (a.gk) { unpack8(ld16(a.gk + go), g);
+    for (int e = 0; e < 8; ++e) fq[e] = fmaf(g[e], w, fq[e]);
+    unpack8(gk[l], g);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) fk[e] = fmaf(g[e], w, fk[e]); }
-    if (a.gv) { unpack8(ld16(a.gv + go), g);
+    for (int e = 0; e < 8; ++e) fk[e] = fmaf(g[e], w, fk[e]);
+    unpack8(gv[l], g);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) fv[e] = fmaf(g[e], w, fv[e]); }
+    for (int e = 0; e < 8; ++e) fv[e] = fmaf(g[e], w, fv[e]);
   }
   const size_t o = (size_t)row * LH_D + 8 * l16;
   if (a.dq) *reinterpret_cast<uint4*>(a.dq + o) = pack8(fq);
@@ -231,7 +245,18 @@ extern "C" int lh_pyramid_bwd(const void* gq, const void* gk, const void* gv, in
   a.rows = (long long)B * S * H;
   const long long blocks = (a.rows + 15) / 16;
   if (blocks > 2147483647LL) return LH_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(pyramid_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)blocks), blk(256);
+  switch (L) {
+    case 1: hipLaunchKernelGGL(pyramid_bwd_kernel<1>, grid, blk, 0, st, a); break;
+    case 2: hipLaunchKernelGGL(pyramid_bwd_kernel<2>, grid, blk, 0, st, a); break;
+    case 3: hipLaunchKernelGGL(pyramid_bwd_kernel<3>, grid, blk, 0, st, a); break;
+    case 4: hipLaunchKernelGGL(pyramid_bwd_kernel<4>, grid, blk, 0, st, a); break;
+    case 5: hipLaunchKernelGGL(pyramid_bwd_kernel<5>, grid, blk, 0, st, a); break;
+    case 6: hipLaunchKernelGGL(pyramid_bwd_kernel<6>, grid, blk, 0, st, a); break;
+    case 7: hipLaunchKernelGGL(pyramid_bwd_kernel<7>, grid, blk, 0, st, a); break;
+    default: hipLaunchKernelGGL(pyramid_bwd_kernel<8>, grid, blk, 0, st, a); break;
+  }
   LH_CHECK_LAUNCH();
   return LH_OK;
 }
