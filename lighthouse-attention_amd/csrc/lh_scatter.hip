@@ -27,6 +27,9 @@ struct ScatArgs {
 
 __device__ __forceinline__ uint4 ld16(const bf16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
+// Forward: all levels' inverse lookups first, then all row loads (two
+// dependent memory round trips per output row instead of two per level).
+template <int NL>
 __global__ __launch_bounds__(256) void scatter_fwd_kernel(const ScatArgs a) {
   const int tid = threadIdx.x;
   const long long row = (long long)blockIdx.x * 16 + (tid >> 4);
@@ -36,21 +39,29 @@ __global__ __launch_bounds__(256) void scatter_fwd_kernel(const ScatArgs a) {
   const long long bh = row / a.S_out;
   const int32_t* inv = a.map + bh * a.S_tot;
   const bf16_t* src = a.src + (size_t)bh * a.n * LH_D + 8 * l16;
+  int s[NL];
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+    const int node = ((t + 1) >> (l * a.shift)) - 1;
+    s[l] = (node >= 0 && node < a.len[l + 1]) ? inv[a.off[l + 1] + node] : -1;
+  }
+  uint4 v[NL];
+#pragma unroll
+  for (int l = 0; l < NL; ++l) v[l] = s[l] >= 0 ? ld16(src + (size_t)s[l] * LH_D) : make_uint4(0, 0, 0, 0);
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int lvl = 1; lvl <= a.L; ++lvl) {
-    const int cs = (lvl - 1) * a.shift;
-    const int node = ((t + 1) >> cs) - 1;
-    if (node < 0 || node >= a.len[lvl]) continue;
-    const int s = inv[a.off[lvl] + node];
-    if (s < 0) continue;
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+    if (s[l] < 0) continue;  // keeps the fp32 sum of exactly the present terms
     float f[8];
-    unpack8(ld16(src + (size_t)s * LH_D), f);
+    unpack8(v[l], f);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] += f[e];
   }
   *reinterpret_cast<uint4*>(a.dst + (size_t)row * LH_D + 8 * l16) = pack8(acc);
 }
 
+// Backward: the span's dout rows are loaded four at a time (independent
+// loads), and the attention-output row for delta is loaded up front.
 __global__ __launch_bounds__(256) void scatter_bwd_kernel(const ScatArgs a) {
   const int tid = threadIdx.x;
   const long long row = (long long)blockIdx.x * 16 + (tid >> 4);
@@ -58,6 +69,8 @@ __global__ __launch_bounds__(256) void scatter_bwd_kernel(const ScatArgs a) {
   if (row >= a.rows) return;  // all 16 lanes of a row leave together
   const long long bh = row / a.n;
   const int r = a.map[row];
+  uint4 ov = make_uint4(0, 0, 0, 0);
+  if (a.delta) ov = ld16(a.o + (size_t)row * LH_D + 8 * l16);
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   if (r >= 0 && r < a.S_tot) {
     int lvl = 1;
@@ -68,11 +81,18 @@ __global__ __launch_bounds__(256) void scatter_bwd_kernel(const ScatArgs a) {
     const int start = local * c + c - 1;
     const int stop = min(start + c, a.S_out);
     const bf16_t* src = a.src + (size_t)bh * a.S_out * LH_D + 8 * l16;
-    for (int t = start; t < stop; ++t) {
-      float f[8];
-      unpack8(ld16(src + (size_t)t * LH_D), f);
+    for (int t = start; t < stop; t += 4) {
+      uint4 v[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += f[e];
+      for (int u = 0; u < 4; ++u) v[u] = t + u < stop ? ld16(src + (size_t)(t + u) * LH_D) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (t + u >= stop) break;  // same left-to-right fp32 sum as one row at a time
+        float f[8];
+        unpack8(v[u], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += f[e];
+      }
     }
   }
   const uint4 packed = pack8(acc);
@@ -80,7 +100,7 @@ __global__ __launch_bounds__(256) void scatter_bwd_kernel(const ScatArgs a) {
   if (a.delta) {
     float g[8], o[8];
     unpack8(packed, g);
-    unpack8(ld16(a.o + (size_t)row * LH_D + 8 * l16), o);
+    unpack8(ov, o);
     float d = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) d = fmaf(g[e], o[e], d);
@@ -113,7 +133,18 @@ extern "C" int lh_scatter_fwd(const void* attn, const int32_t* inverse, void* ou
   a.rows = (long long)B * H * S_out;
   const long long blocks = (a.rows + 15) / 16;
   if (blocks > 2147483647LL) return LH_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(scatter_fwd_kernel, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)blocks), blk(256);
+  switch (L) {
+    case 1: hipLaunchKernelGGL(scatter_fwd_kernel<1>, grid, blk, 0, st, a); break;
+    case 2: hipLaunchKernelGGL(scatter_fwd_kernel<2>, grid, blk, 0, st, a); break;
+    case 3: hipLaunchKernelGGL(scatter_fwd_kernel<3>, grid, blk, 0, st, a); break;
+    case 4: hipLaunchKernelGGL(scatter_fwd_kernel<4>, grid, blk, 0, st, a); break;
+    case 5: hipLaunchKernelGGL(scatter_fwd_kernel<5>, grid, blk, 0, st, a); break;
+    case 6: hipLaunchKernelGGL(scatter_fwd_kernel<6>, grid, blk, 0, st, a); break;
+    case 7: hipLaunchKernelGGL(scatter_fwd_kernel<7>, grid, blk, 0, st, a); break;
+    default: hipLaunchKernelGGL(scatter_fwd_kernel<8>, grid, blk, 0, st, a); break;
+  }
   LH_CHECK_LAUNCH();
   return LH_OK;
 }
