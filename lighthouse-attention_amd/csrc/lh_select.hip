@@ -40,13 +40,35 @@ struct SelParams {
 };
 
 // ---------------------------------------------------------------------------
-// compare-exchange at lane distance j (1..32) for one slot
+// Value of lane ^ J without a round trip through LDS: DPP quad permutes for 1
+// and 2, a 16-lane row rotation by 8 for 8, the gfx950 row/half swaps for 16
+// and 32; only 4 uses ds_swizzle (no memory access).
 // ---------------------------------------------------------------------------
-template <int TIE>
-__device__ __forceinline__ void cx_lane(float& s, int& x, int& id, int j, bool desc, int lane) {
-  const float os = __shfl_xor(s, j);
-  const int ox = __shfl_xor(x, j);
-  const int oid = TIE ? __shfl_xor(id, j) : 0;
+template <int J>
+__device__ __forceinline__ int lane_xor(int v, int lane) {
+  if constexpr (J == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);  // quad_perm [1,0,3,2]
+  else if constexpr (J == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);  // quad_perm [2,3,0,1]
+  else if constexpr (J == 4) return __builtin_amdgcn_ds_swizzle(v, 0x101F);  // swap groups of 4 (xor mask 4)
+  else if constexpr (J == 8) return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, true);  // row_ror:8
+  else if constexpr (J == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane & 16) ? (int)r[0] : (int)r[1];
+  } else {
+    static_assert(J == 32, "lane distance");
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane & 32) ? (int)r[0] : (int)r[1];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// compare-exchange at lane distance J (1..32) for one slot
+// ---------------------------------------------------------------------------
+template <int TIE, int J>
+__device__ __forceinline__ void cx_lane(float& s, int& x, int& id, bool desc, int lane) {
+  const float os = __int_as_float(lane_xor<J>(__float_as_int(s), lane));
+  const int ox = lane_xor<J>(x, lane);
+  const int oid = TIE ? lane_xor<J>(id, lane) : 0;
+  const int j = J;
   const bool keep_max = (((lane & j) == 0) == desc);
   bool take;
   if (TIE == LH_TIE_REFERENCE) {
@@ -60,33 +82,40 @@ __device__ __forceinline__ void cx_lane(float& s, int& x, int& id, int j, bool d
   if (take) { s = os; x = ox; id = oid; }
 }
 
+// One stage (k, j) of the descending 128-wide bitonic sort; element e = 64*slot + lane.
+template <int TIE, int K, int J>
+__device__ __forceinline__ void sort_stage(float& s0, int& x0, int& i0, float& s1, int& x1, int& i1, int lane) {
+  if constexpr (J == 64) {  // k == 128: pair (lane, 64 + lane), descending
+    bool take;
+    if (TIE == LH_TIE_REFERENCE) {
+      take = s0 < s1;
+    } else {
+      take = (s1 > s0) || (s1 == s0 && (unsigned)i1 < (unsigned)i0);
+    }
+    if (take) {
+      float ts = s0; s0 = s1; s1 = ts;
+      int tx = x0; x0 = x1; x1 = tx;
+      int ti = i0; i0 = i1; i1 = ti;
+    }
+  } else {
+    const bool desc0 = (K >= 64) ? true : ((lane & K) == 0);
+    const bool desc1 = (K == 128) ? true : (K == 64 ? false : ((lane & K) == 0));
+    cx_lane<TIE, J>(s0, x0, i0, desc0, lane);
+    cx_lane<TIE, J>(s1, x1, i1, desc1, lane);
+  }
+  if constexpr (J > 1) sort_stage<TIE, K, J / 2>(s0, x0, i0, s1, x1, i1, lane);
+}
+
+template <int TIE, int K>
+__device__ __forceinline__ void sort_from(float& s0, int& x0, int& i0, float& s1, int& x1, int& i1, int lane) {
+  sort_stage<TIE, K, K / 2>(s0, x0, i0, s1, x1, i1, lane);
+  if constexpr (K < TOPK) sort_from<TIE, 2 * K>(s0, x0, i0, s1, x1, i1, lane);
+}
+
 // Descending 128-wide bitonic sort; element e = 64*slot + lane.
 template <int TIE>
 __device__ __forceinline__ void sort128(float& s0, int& x0, int& i0, float& s1, int& x1, int& i1, int lane) {
-#pragma unroll
-  for (int k = 2; k <= TOPK; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      if (j == 64) {  // k == 128: pair (lane, 64 + lane), descending
-        bool take;
-        if (TIE == LH_TIE_REFERENCE) {
-          take = s0 < s1;
-        } else {
-          take = (s1 > s0) || (s1 == s0 && (unsigned)i1 < (unsigned)i0);
-        }
-        if (take) {
-          float ts = s0; s0 = s1; s1 = ts;
-          int tx = x0; x0 = x1; x1 = tx;
-          int ti = i0; i0 = i1; i1 = ti;
-        }
-      } else {
-        const bool desc0 = (k >= 64) ? true : ((lane & k) == 0);
-        const bool desc1 = (k == 128) ? true : (k == 64 ? false : ((lane & k) == 0));
-        cx_lane<TIE>(s0, x0, i0, j, desc0, lane);
-        cx_lane<TIE>(s1, x1, i1, j, desc1, lane);
-      }
-    }
-  }
+  sort_from<TIE, 2>(s0, x0, i0, s1, x1, i1, lane);
 }
 
 __device__ __forceinline__ bool get_bit(const uint32_t* bits, int i) {
