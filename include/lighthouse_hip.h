@@ -160,9 +160,11 @@ int lh_attn_bwd_dq(const void *q, const void *k, const void *v, int64_t sb, int6
  * out[b,h,t] = sum over levels l of attn[b,h,inverse[b,h,off_l + (t+1)/c_l - 1]].
  * Replaces _scatter_fanout_fwd_kernel / _ScatterToBaseAutograd.forward
  * (src/lighthouse_selection.py:408-459, :519-550) without atomics.
- *   attn bf16 [B, H, n, D]; out bf16 [B, H, S_out, D] (rows >= S are zero)
+ *   attn bf16 [B, H, n, D]; out bf16 [B, H, S_out, D] logically (rows >= S are zero),
+ *   element (b, h, t, :) at out + b*ob + h*oh + t*os (D contiguous): (H*S_out*D, S_out*D, D)
+ *   for [B, H, S_out, D] storage, (S_out*H*D, D, H*D) for [B, S_out, H, D] storage.
  */
-int lh_scatter_fwd(const void *attn, const int32_t *inverse, void *out,
+int lh_scatter_fwd(const void *attn, const int32_t *inverse, void *out, int64_t ob, int64_t oh, int64_t os,
                    int B, int H, int S, int S_out, int n, int D, int L, int p, void *stream);
 
 /*
@@ -170,9 +172,9 @@ int lh_scatter_fwd(const void *attn, const int32_t *inverse, void *out,
  * plus delta[s] = sum_d bf16(dattn[s,d]) * o[s,d] for the attention backward
  * (delta is skipped when o or delta is NULL).
  * Replaces _scatter_fanout_bwd_kernel (src/lighthouse_selection.py:462-514, :552-576).
- *   dout bf16 [B, H, S_out, D]
+ *   dout bf16 [B, H, S_out, D] logically, element (b, h, t, :) at dout + b*db + h*dh + t*ds
  */
-int lh_scatter_bwd(const void *dout, const int32_t *indices, const void *o,
+int lh_scatter_bwd(const void *dout, int64_t db, int64_t dh, int64_t ds, const int32_t *indices, const void *o,
                    void *dattn, float *delta,
                    int B, int H, int S, int S_out, int n, int D, int L, int p, void *stream);
 
@@ -241,6 +243,13 @@ int lh_swiglu_fwd(const void *h, void *a, int64_t rows, int F, void *stream);
 
 /* SwiGLU backward into the fused layout: dh = [dh1 | dh3] (rows of 2F). */
 int lh_swiglu_bwd(const void *da, const void *h, void *dh, int64_t rows, int F, void *stream);
+
+/*
+ * Sum of split-K partial products: out[i] = bf16(sum_s part[s][i]) for the
+ * projections' weight gradients computed in token slices (fp32 [splits, n],
+ * n a multiple of 8).  Replaces part.sum(0).to(bfloat16).
+ */
+int lh_splitk_sum(const float *part, void *out, int splits, int64_t n, void *stream);
 
 #ifdef __cplusplus
 }

@@ -49,8 +49,8 @@ _SIGS = {
                               _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P]),
     "lh_attn_bwd_dq": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _I, _P,
                             _I, _I, _I, _I, _F, _P, _P, _P, _P, _P]),
-    "lh_scatter_fwd": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
-    "lh_scatter_bwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_scatter_fwd": (_I, [_P, _P, _P, _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_scatter_bwd": (_I, [_P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_pyramid_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "lh_rope_qkv_fwd": (_I, [_P, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "lh_rope_qkv_bwd": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P]),
@@ -58,6 +58,7 @@ _SIGS = {
     "lh_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _P]),
     "lh_swiglu_fwd": (_I, [_P, _P, _L, _I, _P]),
     "lh_swiglu_bwd": (_I, [_P, _P, _P, _L, _I, _P]),
+    "lh_splitk_sum": (_I, [_P, _P, _I, _L, _P]),
 }
 EXPORTED = tuple(_SIGS)
 
@@ -304,30 +305,41 @@ def attn_bwd(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D: i
     return dq, dk, dv
 
 
-def scatter_fwd(attn, inverse, S: int, S_out: int, L: int, p: int):
+def scatter_fwd(attn, inverse, S: int, S_out: int, L: int, p: int, seq_major: bool = False):
+    """Fan-out of the selected rows onto the base sequence: ``[B, H, S_out, D]``.
+
+    ``seq_major`` stores the result as ``[B, S_out, H, D]`` and returns its
+    ``[B, H, S_out, D]`` view (transposing it back is then free)."""
     _need_gpu(attn, inverse)
     attn = attn.contiguous()
     B, H, n, D = attn.shape
-    out = torch.empty(B, H, S_out, D, dtype=attn.dtype, device=attn.device)
+    if seq_major:
+        out = torch.empty(B, S_out, H, D, dtype=attn.dtype, device=attn.device).transpose(1, 2)
+    else:
+        out = torch.empty(B, H, S_out, D, dtype=attn.dtype, device=attn.device)
+    ob, oh, os_, od = out.stride()
     with torch.cuda.device(attn.device):
-        rc = lib().lh_scatter_fwd(_ptr(attn), _ptr(inverse), _ptr(out), B, H, S, S_out, n, D, L, p,
+        rc = lib().lh_scatter_fwd(_ptr(attn), _ptr(inverse), _ptr(out), ob, oh, os_, B, H, S, S_out, n, D, L, p,
                                   _stream(attn.device))
     _check(rc, "lh_scatter_fwd")
     return out
 
 
 def scatter_bwd(dout, indices, o, S: int, L: int, p: int):
-    """``(dattn bf16 [B, H, n, D], delta fp32 [B, H, n] or None)``."""
+    """``(dattn bf16 [B, H, n, D], delta fp32 [B, H, n] or None)``; ``dout`` may have
+    any (batch, head, seq) strides with D contiguous."""
     _need_gpu(dout, indices)
-    dout = dout.contiguous()
+    if dout.stride(3) != 1 or any(st % 8 for st in dout.stride()[:3]) or dout.data_ptr() % 16:
+        dout = dout.contiguous()
     B, H, S_out, D = dout.shape
     n = indices.shape[-1]
     dattn = torch.empty(B, H, n, D, dtype=dout.dtype, device=dout.device)
     delta = torch.empty(B, H, n, dtype=torch.float32, device=dout.device) if o is not None else None
     oc = o.contiguous() if o is not None else None
+    db, dh, ds, _ = dout.stride()
     with torch.cuda.device(dout.device):
-        rc = lib().lh_scatter_bwd(_ptr(dout), _ptr(indices.contiguous()), _ptr(oc), _ptr(dattn), _ptr(delta),
-                                  B, H, S, S_out, n, D, L, p, _stream(dout.device))
+        rc = lib().lh_scatter_bwd(_ptr(dout), db, dh, ds, _ptr(indices.contiguous()), _ptr(oc), _ptr(dattn),
+                                  _ptr(delta), B, H, S, S_out, n, D, L, p, _stream(dout.device))
     _check(rc, "lh_scatter_bwd")
     return dattn, delta
 
@@ -452,3 +464,14 @@ def swiglu_bwd(da, h):
         rc = lib().lh_swiglu_bwd(_ptr(da), _ptr(h), _ptr(dh), rows, F2 // 2, _stream(h.device))
     _check(rc, "lh_swiglu_bwd")
     return dh
+
+
+def splitk_sum(part):
+    """``part`` fp32 [s, ...] -> bf16 sum over s (one rounding)."""
+    _need_gpu(part)
+    part = part.contiguous()
+    out = torch.empty(part.shape[1:], dtype=torch.bfloat16, device=part.device)
+    with torch.cuda.device(part.device):
+        rc = lib().lh_splitk_sum(_ptr(part), _ptr(out), part.shape[0], out.numel(), _stream(part.device))
+    _check(rc, "lh_splitk_sum")
+    return out

@@ -42,6 +42,8 @@ def _wgrad(dy2, x2):
     if s == 1:
         return dy2.t() @ x2
     part = torch.bmm(dy2.view(s, T // s, O).transpose(1, 2), x2.view(s, T // s, I), out_dtype=torch.float32)
+    if (O * I) % 8 == 0:
+        return N.splitk_sum(part)
     return part.sum(0).to(dy2.dtype)
 
 

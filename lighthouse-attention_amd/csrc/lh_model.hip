@@ -259,6 +259,25 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const bf16_t* __restrict__ 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Split-K weight gradient: out[i] = bf16(sum over s of part[s][i]), fp32 sum in
+// slice order (what one accumulation over the whole token axis would give up
+// to fp32 reassociation), 8 outputs per lane.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict__ part, bf16_t* __restrict__ out,
+                                                         int splits, int64_t n) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * kVec;
+  if (i >= n) return;
+  float acc[kVec] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int sp = 0; sp < splits; ++sp) {
+    const float4* p = reinterpret_cast<const float4*>(part + (int64_t)sp * n + i);
+    const float4 a = p[0], b = p[1];
+    acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
+    acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+  }
+  st16(out + i, pack8(acc));
+}
+
 inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 inline int grid_of(int64_t n) { return (int)((n + 255) / 256); }
@@ -368,6 +387,15 @@ extern "C" int lh_swiglu_bwd(const void* da, const void* h, void* dh, int64_t ro
   if (n / 256 + 1 > 0x7fffffffLL) return LH_ERR_UNSUPPORTED;
   swiglu_kernel<false><<<grid_of(n), 256, 0, (hipStream_t)stream>>>((const bf16_t*)h, (const bf16_t*)da, (bf16_t*)dh,
                                                                      rows, F);
+  LH_CHECK_LAUNCH();
+  return LH_OK;
+}
+
+extern "C" int lh_splitk_sum(const float* part, void* out, int splits, int64_t n, void* stream) {
+  if (!part || !out || splits <= 0 || n <= 0 || n % 8 || !al16(part) || !al16(out)) return LH_ERR_INVALID_ARG;
+  const int64_t threads = n / kVec;
+  if (threads / 256 + 1 > 0x7fffffffLL) return LH_ERR_UNSUPPORTED;
+  splitk_sum_kernel<<<grid_of(threads), 256, 0, (hipStream_t)stream>>>(part, (bf16_t*)out, splits, n);
   LH_CHECK_LAUNCH();
   return LH_OK;
 }

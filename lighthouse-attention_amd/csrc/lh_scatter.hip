@@ -15,12 +15,13 @@
 namespace {
 
 struct ScatArgs {
-  const bf16_t* src;       // fwd: attn [BH, n, D];  bwd: dout [BH, S_out, D]
+  const bf16_t* src;       // fwd: attn [BH, n, D];  bwd: dout, [b, h, t] at b*sb + h*sh + t*st
   const int32_t* map;      // fwd: inverse [BH, S_tot];  bwd: indices [BH, n]
   const bf16_t* o;         // bwd: attention output [BH, n, D] (optional)
-  bf16_t* dst;             // fwd: out [BH, S_out, D];  bwd: dattn [BH, n, D]
+  bf16_t* dst;             // fwd: out, [b, h, t] at b*sb + h*sh + t*st;  bwd: dattn [BH, n, D]
   float* delta;            // bwd: [BH, n] (optional)
-  int S, S_out, n, L, shift, S_tot;
+  int64_t sb, sh, st;      // element strides of the base-sequence tensor (D contiguous)
+  int H, S, S_out, n, L, shift, S_tot;
   int off[9], len[9];
   long long rows;
 };
@@ -57,7 +58,8 @@ __global__ __launch_bounds__(256) void scatter_fwd_kernel(const ScatArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] += f[e];
   }
-  *reinterpret_cast<uint4*>(a.dst + (size_t)row * LH_D + 8 * l16) = pack8(acc);
+  const int b = (int)(bh / a.H), h = (int)(bh % a.H);
+  *reinterpret_cast<uint4*>(a.dst + b * a.sb + h * a.sh + t * a.st + 8 * l16) = pack8(acc);
 }
 
 // Backward: the span's dout rows are loaded four at a time (independent
@@ -80,11 +82,12 @@ __global__ __launch_bounds__(256) void scatter_bwd_kernel(const ScatArgs a) {
     const int local = r - a.off[lvl];
     const int start = local * c + c - 1;
     const int stop = min(start + c, a.S_out);
-    const bf16_t* src = a.src + (size_t)bh * a.S_out * LH_D + 8 * l16;
+    const int b = (int)(bh / a.H), h = (int)(bh % a.H);
+    const bf16_t* src = a.src + b * a.sb + h * a.sh + 8 * l16;
     for (int t = start; t < stop; t += 4) {
       uint4 v[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = t + u < stop ? ld16(src + (size_t)(t + u) * LH_D) : make_uint4(0, 0, 0, 0);
+      for (int u = 0; u < 4; ++u) v[u] = t + u < stop ? ld16(src + (t + u) * a.st) : make_uint4(0, 0, 0, 0);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         if (t + u >= stop) break;  // same left-to-right fp32 sum as one row at a time
@@ -110,11 +113,13 @@ __global__ __launch_bounds__(256) void scatter_bwd_kernel(const ScatArgs a) {
   }
 }
 
-int fill(ScatArgs& a, int S, int S_out, int n, int L, int p, int B, int H) {
+int fill(ScatArgs& a, int S, int S_out, int n, int L, int p, int B, int H, int64_t sb, int64_t sh, int64_t st) {
   const int shift = ilog2_exact(p);
   if (shift <= 0 || L < 1 || L > 8 || S <= 0 || S_out <= 0 || n < 0 || B <= 0 || H <= 0) return LH_ERR_INVALID_ARG;
+  if ((sb | sh | st) % 8 || sb < 0 || sh < 0 || st <= 0) return LH_ERR_INVALID_ARG;
   Pyramid g;
   if (!make_pyramid(S, L, p, &g)) return LH_ERR_INVALID_ARG;
+  a.sb = sb; a.sh = sh; a.st = st; a.H = H;
   a.S = S; a.S_out = S_out; a.n = n; a.L = L; a.shift = shift; a.S_tot = g.total;
   for (int l = 1; l <= L; ++l) { a.off[l] = g.off[l]; a.len[l] = g.len[l]; }
   return LH_OK;
@@ -122,12 +127,12 @@ int fill(ScatArgs& a, int S, int S_out, int n, int L, int p, int B, int H) {
 
 }  // namespace
 
-extern "C" int lh_scatter_fwd(const void* attn, const int32_t* inverse, void* out, int B, int H, int S, int S_out,
-                              int n, int D, int L, int p, void* stream) {
+extern "C" int lh_scatter_fwd(const void* attn, const int32_t* inverse, void* out, int64_t ob, int64_t oh,
+                              int64_t os, int B, int H, int S, int S_out, int n, int D, int L, int p, void* stream) {
   if (D != LH_D) return LH_ERR_UNSUPPORTED;
-  if (!attn || !inverse || !out) return LH_ERR_INVALID_ARG;
+  if (!attn || !inverse || !out || ((uintptr_t)out & 15)) return LH_ERR_INVALID_ARG;
   ScatArgs a{};
-  int rc = fill(a, S, S_out, n, L, p, B, H);
+  int rc = fill(a, S, S_out, n, L, p, B, H, ob, oh, os);
   if (rc) return rc;
   a.src = (const bf16_t*)attn; a.map = inverse; a.dst = (bf16_t*)out;
   a.rows = (long long)B * H * S_out;
@@ -149,12 +154,14 @@ extern "C" int lh_scatter_fwd(const void* attn, const int32_t* inverse, void* ou
   return LH_OK;
 }
 
-extern "C" int lh_scatter_bwd(const void* dout, const int32_t* indices, const void* o, void* dattn, float* delta,
-                              int B, int H, int S, int S_out, int n, int D, int L, int p, void* stream) {
+extern "C" int lh_scatter_bwd(const void* dout, int64_t db, int64_t dh, int64_t ds, const int32_t* indices,
+                              const void* o, void* dattn, float* delta, int B, int H, int S, int S_out, int n, int D,
+                              int L, int p, void* stream) {
   if (D != LH_D) return LH_ERR_UNSUPPORTED;
-  if (!dout || !indices || !dattn || ((o == nullptr) != (delta == nullptr))) return LH_ERR_INVALID_ARG;
+  if (!dout || !indices || !dattn || ((o == nullptr) != (delta == nullptr)) || ((uintptr_t)dout & 15))
+    return LH_ERR_INVALID_ARG;
   ScatArgs a{};
-  int rc = fill(a, S, S_out, n, L, p, B, H);
+  int rc = fill(a, S, S_out, n, L, p, B, H, db, dh, ds);
   if (rc) return rc;
   a.src = (const bf16_t*)dout; a.map = indices; a.o = (const bf16_t*)o; a.dst = (bf16_t*)dattn; a.delta = delta;
   a.rows = (long long)B * H * n;

@@ -124,7 +124,7 @@ class _LighthouseLayerFn(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, xq, xk, xv, L, p, topk, tie, strict, dilation):
+    def forward(ctx, xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major):
         B, S, H, D = xq.shape
         xq, xk, xv = xq.contiguous(), xk.contiguous(), xv.contiguous()
         lens, offs, S_tot = N.pyramid_lengths(S, L, p)
@@ -142,7 +142,7 @@ class _LighthouseLayerFn(torch.autograd.Function):
         rows = _base_rows(xq, xk, xv, pq, pk, pv)
         o, lse = N.attn_fwd(rows, idx, B, H, S_sel, D)
         _mark("attn_fwd")
-        out = N.scatter_fwd(o, inv, S, S, L, p)
+        out = N.scatter_fwd(o, inv, S, S, L, p, seq_major=seq_major)
         _mark("scatter_fwd")
         ctx.save_for_backward(xq, xk, xv, pq, pk, pv, idx, inv, o, lse)
         ctx.geo = (B, S, H, D, L, p, S_sel)
@@ -155,7 +155,7 @@ class _LighthouseLayerFn(torch.autograd.Function):
         xq, xk, xv, pq, pk, pv, idx, inv, o, lse = ctx.saved_tensors
         B, S, H, D, L, p, S_sel = ctx.geo
         if dout is None:
-            return None, None, None, None, None, None, None, None, None
+            return None, None, None, None, None, None, None, None, None, None
         _mark("bwd_start")
         dattn, delta = N.scatter_bwd(dout, idx, o, S, L, p)
         _mark("scatter_bwd")
@@ -166,14 +166,17 @@ class _LighthouseLayerFn(torch.autograd.Function):
         _mark("attn_bwd_dq")
         dxq, dxk, dxv = N.pyramid_bwd(dqs, dks, dvs, inv, B, S, H, L, p, D)
         _mark("pyramid_bwd")
-        return dxq, dxk, dxv, None, None, None, None, None, None
+        return dxq, dxk, dxv, None, None, None, None, None, None, None
 
 
 def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, topk: int = 1024,
-                     tie_break: str = "reference", strict: bool = True, dilation: int = 0):
+                     tie_break: str = "reference", strict: bool = True, dilation: int = 0,
+                     seq_major: bool = False):
     """Functional form of the native layer: ``(out [B, H, S, D], indices [B, H, S_sel])``.
 
-    ``dilation > 0`` selects the dilated scorer, 0 the norm scorer."""
+    ``dilation > 0`` selects the dilated scorer, 0 the norm scorer.  ``seq_major``
+    stores ``out`` as ``[B, S, H, D]`` (the returned tensor is its ``[B, H, S, D]``
+    view), which is the layout the model's output projection reads."""
     if xq.shape[-1] != N.D_SUPPORTED:
         raise ValueError(f"head_dim must be {N.D_SUPPORTED}, got {xq.shape[-1]}")
     if not (xq.shape == xk.shape == xv.shape):
@@ -182,7 +185,7 @@ def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, t
         if t.dtype != torch.bfloat16:
             raise TypeError("the native layer computes in bfloat16; got " + str(t.dtype))
     return _LighthouseLayerFn.apply(xq, xk, xv, num_levels, pooling_factor, topk, tie_break, strict,
-                                    int(dilation))
+                                    int(dilation), bool(seq_major))
 
 
 class _PyramidCatFn(torch.autograd.Function):
@@ -379,6 +382,9 @@ class LighthouseLocal(nn.Module):
         self.strict = strict
         self.use_native_attention = use_native_attention
         self.last_indices = None
+        # True: the fused path stores its output as [B, S, H, D] and returns the
+        # [B, H, S, D] view (same values and shape, strided)
+        self.out_seq_major = False
 
     def _native_dilation(self):
         sc = self.scorer
@@ -394,7 +400,7 @@ class LighthouseLocal(nn.Module):
         if self.use_native_attention and dil is not None and \
                 self.scorer.levels == self.num_levels and self.scorer.pooling_factor == self.pooling_factor:
             out, idx = lighthouse_layer(xq, xk, xv, self.num_levels, self.pooling_factor, self.topk,
-                                        self.tie_break, self.strict, dil)
+                                        self.tie_break, self.strict, dil, self.out_seq_major)
             self.last_indices = idx
             return out
         # generic composition, as in the reference, for scorers and attentions from elsewhere

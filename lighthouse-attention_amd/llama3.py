@@ -264,6 +264,9 @@ class Attention(nn.Module):
                                                   attention=self.inner_attention,
                                                   tie_break=args.lighthouse_tie_break,
                                                   strict=args.lighthouse_strict)
+            # the output goes straight into wo: store it sequence-major, so the
+            # transpose below is free in both directions
+            self.selection_attn.out_seq_major = True
 
     def init_weights(self, init_std: float):
         for lin in (self.wq, self.wk, self.wv):

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol(pkg):
     for n in _declared():
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
     assert set(_declared()) == set(pkg._native.EXPORTED)
-    assert lib.lh_abi_version() == 1
+    assert lib.lh_abi_version() == 2
 
 
 def test_strerror(pkg):
@@ -74,7 +74,7 @@ def test_host_validation_rejects_before_launch(pkg):
     assert lib.lh_select_topk(null, null, null, null, 1, 1, 4096, 3, 4, 256, 0, 1, null) == 1
     assert lib.lh_pyramid_fwd(null, null, null, 0, 0, 0, null, null, null, 0, 0, 0, null, null,
                               1, 1024, 1, 128, 3, 4, 0, null) == 1
-    assert lib.lh_scatter_fwd(null, null, null, 1, 1, 1024, 1024, 10, 64, 3, 4, null) == 4
+    assert lib.lh_scatter_fwd(null, null, null, 0, 0, 0, 1, 1, 1024, 1024, 10, 64, 3, 4, null) == 4
     assert lib.lh_pyramid_bwd(null, null, null, 0, 0, 0, null, null, null, null, 1, 1024, 1, 128, 3, 3,
                               null) == 1
     assert lib.lh_select_geometry(4096, 3, 4, 1536, 1, None, None, None, None) == 2
@@ -86,6 +86,7 @@ def test_host_validation_rejects_before_launch(pkg):
     assert lib.lh_rmsnorm_bwd(null, null, null, null, null, null, null, 4, 16, 1024, null) == 1
     assert lib.lh_swiglu_fwd(null, null, 16, 1024, null) == 1
     assert lib.lh_swiglu_bwd(null, null, null, 16, 1000, null) == 1
+    assert lib.lh_splitk_sum(null, null, 4, 1024, null) == 1
     # a row too long for one wave's registers is refused as unsupported
     x = (ctypes.c_uint16 * 1024)()
     r = (ctypes.c_float * 4)()

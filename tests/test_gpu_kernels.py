@@ -91,6 +91,13 @@ def test_scatter_fwd_bwd(pkg, dev, S, L, p, k, S_out):
     assert_close(dattn, ref_d, "scatter bwd", max_abs=8e-3, rel_l2=4e-3)
     ref_delta = (dattn.float().cpu() * o.float()).sum(-1)
     assert_close(delta, ref_delta, "delta", max_abs=1e-4, rel_l2=1e-5)
+    # sequence-major storage ([B, S, H, D]) of the output and of the incoming gradient
+    out_sm = pkg._native.scatter_fwd(attn.to(dev), inv, S, S_out, L, p, seq_major=True)
+    assert out_sm.shape == out.shape and out_sm.transpose(1, 2).is_contiguous()
+    assert torch.equal(out_sm, out)
+    dout_sm = dout.to(dev).transpose(1, 2).contiguous().transpose(1, 2)
+    dattn_sm, delta_sm = pkg._native.scatter_bwd(dout_sm, idx_t.to(dev), o.to(dev), S, L, p)
+    assert torch.equal(dattn_sm, dattn) and torch.equal(delta_sm, delta)
 
 
 def _attn_case(pkg, dev, S, L, p, k, H, seed):
