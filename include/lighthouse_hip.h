@@ -229,11 +229,21 @@ int lh_rmsnorm_fwd(const void *x, const void *w, void *y, float *rstd, int64_t r
                    void *stream);
 
 /*
- * RMSNorm backward: dx = r g - x r^3 mean(g x) with g = dy w; dw = sum_rows dy x r.
- * dw_part is caller workspace, fp32 [dim, parts]; dw is bf16 [dim].
+ * Residual add fused with the RMSNorm that follows it: h = bf16(x + r) is written
+ * out, and y = RMSNorm(h) as lh_rmsnorm_fwd.  Replaces `h = x + attn(...)` followed
+ * by `ffn_norm(h)` (and the next block's `attention_norm`) in the Llama3 block.
  */
-int lh_rmsnorm_bwd(const void *dy, const void *x, const void *w, const float *rstd, void *dx, void *dw,
-                   float *dw_part, int parts, int64_t rows, int dim, void *stream);
+int lh_add_rmsnorm_fwd(const void *x, const void *r, const void *w, void *h, void *y, float *rstd,
+                       int64_t rows, int dim, float eps, void *stream);
+
+/*
+ * RMSNorm backward: dx = r g - x r^3 mean(g x) (+ dres) with g = dy w; dw = sum_rows dy x r.
+ * dres (optional, bf16 like dx) is the gradient reaching x through a residual branch,
+ * added in fp32 before the rounding.  dw_part is caller workspace, fp32 [dim, parts];
+ * dw is bf16 [dim].
+ */
+int lh_rmsnorm_bwd(const void *dy, const void *x, const void *w, const float *rstd, const void *dres,
+                   void *dx, void *dw, float *dw_part, int parts, int64_t rows, int dim, void *stream);
 
 /*
  * SwiGLU on the fused [h1 | h3] projection (rows of 2F): a = bf16(bf16(silu(h1)) h3).

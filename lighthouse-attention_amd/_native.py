@@ -55,7 +55,8 @@ _SIGS = {
     "lh_rope_qkv_fwd": (_I, [_P, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "lh_rope_qkv_bwd": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P]),
     "lh_rmsnorm_fwd": (_I, [_P, _P, _P, _P, _L, _I, _F, _P]),
-    "lh_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _P]),
+    "lh_add_rmsnorm_fwd": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _F, _P]),
+    "lh_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _P]),
     "lh_swiglu_fwd": (_I, [_P, _P, _L, _I, _P]),
     "lh_swiglu_bwd": (_I, [_P, _P, _P, _L, _I, _P]),
     "lh_splitk_sum": (_I, [_P, _P, _I, _L, _P]),
@@ -421,13 +422,33 @@ def rmsnorm_fwd(x, w, eps: float):
     return y, rstd
 
 
+def add_rmsnorm_fwd(x, r, w, eps: float):
+    """``h = x + r`` (bf16) and ``y = RMSNorm(h)``; returns ``(h, y, rstd)``."""
+    _need_gpu(x, r, w)
+    x, r = x.contiguous(), r.contiguous()
+    dim = x.shape[-1]
+    rows = x.numel() // dim
+    assert r.shape == x.shape and w.shape == (dim,) and w.is_contiguous()
+    h = torch.empty_like(x)
+    y = torch.empty_like(x)
+    rstd = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib().lh_add_rmsnorm_fwd(_ptr(x), _ptr(r), _ptr(w), _ptr(h), _ptr(y), _ptr(rstd), rows, dim, float(eps),
+                                      _stream(x.device))
+    _check(rc, "lh_add_rmsnorm_fwd")
+    return h, y, rstd
+
+
 RMSNORM_BWD_PARTS = 512
 
 
-def rmsnorm_bwd(dy, x, w, rstd):
-    """Grads of RMSNorm: ``(dx bf16 like x, dw bf16 like w)``."""
+def rmsnorm_bwd(dy, x, w, rstd, dres=None):
+    """Grads of RMSNorm: ``(dx bf16 like x, dw bf16 like w)``; ``dres`` (optional) is
+    added to dx (a residual branch's gradient)."""
     _need_gpu(dy, x, w, rstd)
     dy = dy.contiguous()
+    if dres is not None:
+        dres = dres.contiguous()
     dim = x.shape[-1]
     rows = x.numel() // dim
     dx = torch.empty_like(x)
@@ -435,8 +456,8 @@ def rmsnorm_bwd(dy, x, w, rstd):
     parts = min(RMSNORM_BWD_PARTS, rows)
     part = torch.empty(dim, parts, dtype=torch.float32, device=x.device)
     with torch.cuda.device(x.device):
-        rc = lib().lh_rmsnorm_bwd(_ptr(dy), _ptr(x), _ptr(w), _ptr(rstd), _ptr(dx), _ptr(dw), _ptr(part), parts,
-                                  rows, dim, _stream(x.device))
+        rc = lib().lh_rmsnorm_bwd(_ptr(dy), _ptr(x), _ptr(w), _ptr(rstd), _ptr(dres), _ptr(dx), _ptr(dw),
+                                  _ptr(part), parts, rows, dim, _stream(x.device))
     _check(rc, "lh_rmsnorm_bwd")
     return dx, dw
 

@@ -89,8 +89,10 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(const RopeArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kMaxChunksPerLane = 8;  // dim <= 64 * 8 * 8 = 4096
 
-template <int NC>
-__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
+// With a residual input res (ADD): h = bf16(x + res) is written out and normalised.
+template <int NC, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ res,
+                                                          const bf16_t* __restrict__ w, bf16_t* __restrict__ h,
                                                           bf16_t* __restrict__ y, float* __restrict__ rstd,
                                                           int64_t rows, int dim, float eps) {
   const int lane = threadIdx.x & 63;
@@ -103,6 +105,15 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const bf16_t* __restri
   for (int c = 0; c < NC; ++c) {
     const int col = (c * 64 + lane) * kVec;
     unpack8(col < dim ? ld16(xr + col) : make_uint4(0, 0, 0, 0), v[c]);
+    if (ADD && col < dim) {
+      float rv[kVec];
+      unpack8(ld16(res + row * dim + col), rv);
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) v[c][e] += rv[e];
+      const uint4 hv = pack8(v[c]);
+      st16(h + row * dim + col, hv);
+      unpack8(hv, v[c]);  // normalise the rounded sum, as a separate norm of h would
+    }
 #pragma unroll
     for (int e = 0; e < kVec; ++e) ss += v[c][e] * v[c][e];
   }
@@ -129,8 +140,9 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const bf16_t* __restri
 template <int NC>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const bf16_t* __restrict__ dy, const bf16_t* __restrict__ x,
                                                           const bf16_t* __restrict__ w, const float* __restrict__ rstd,
-                                                          bf16_t* __restrict__ dx, float* __restrict__ dw_part,
-                                                          int64_t rows, int dim, int64_t rows_per_block) {
+                                                          const bf16_t* __restrict__ dres, bf16_t* __restrict__ dx,
+                                                          float* __restrict__ dw_part, int64_t rows, int dim,
+                                                          int64_t rows_per_block) {
   // waves 1..3 hand their dw partials to wave 0, half of the lane's chunks at a time
   __shared__ float red[3][64 * kVec * kMaxChunksPerLane / 2];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -170,7 +182,15 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const bf16_t* __restri
         g[c][e] = r * g[c][e] - xv[c][e] * k3;
       }
       const int col = (c * 64 + lane) * kVec;
-      if (col < dim) st16(dx + row * dim + col, pack8(g[c]));
+      if (col < dim) {
+        if (dres) {  // gradient arriving through the residual branch, summed before one rounding
+          float rv[kVec];
+          unpack8(ld16(dres + row * dim + col), rv);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) g[c][e] += rv[e];
+        }
+        st16(dx + row * dim + col, pack8(g[c]));
+      }
     }
   }
   // reduce the four waves' dw partials through LDS, NC chunks at a time in halves
@@ -347,24 +367,38 @@ extern "C" int lh_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd
   if (dim % 8 || dim > 4096) return LH_ERR_UNSUPPORTED;  // whole 16-byte chunks, <= 8 per lane
   const int nc = (dim + 511) / 512;
   const int grid = (int)((rows + 3) / 4);
-  LH_NC_DISPATCH(nc, (rmsnorm_fwd_kernel<NC><<<grid, 256, 0, (hipStream_t)stream>>>(
-                          (const bf16_t*)x, (const bf16_t*)w, (bf16_t*)y, rstd, rows, dim, eps)));
+  LH_NC_DISPATCH(nc, (rmsnorm_fwd_kernel<NC, false><<<grid, 256, 0, (hipStream_t)stream>>>(
+                          (const bf16_t*)x, nullptr, (const bf16_t*)w, nullptr, (bf16_t*)y, rstd, rows, dim, eps)));
   LH_CHECK_LAUNCH();
   return LH_OK;
 }
 
-extern "C" int lh_rmsnorm_bwd(const void* dy, const void* x, const void* w, const float* rstd, void* dx, void* dw,
-                              float* dw_part, int parts, int64_t rows, int dim, void* stream) {
+extern "C" int lh_add_rmsnorm_fwd(const void* x, const void* r, const void* w, void* h, void* y, float* rstd,
+                                  int64_t rows, int dim, float eps, void* stream) {
+  if (!x || !r || !w || !h || !y || !rstd || rows <= 0 || dim <= 0 || !(eps >= 0.f)) return LH_ERR_INVALID_ARG;
+  if (!al16(x) || !al16(r) || !al16(w) || !al16(h) || !al16(y)) return LH_ERR_INVALID_ARG;
+  if (dim % 8 || dim > 4096) return LH_ERR_UNSUPPORTED;
+  const int nc = (dim + 511) / 512;
+  const int grid = (int)((rows + 3) / 4);
+  LH_NC_DISPATCH(nc, (rmsnorm_fwd_kernel<NC, true><<<grid, 256, 0, (hipStream_t)stream>>>(
+                          (const bf16_t*)x, (const bf16_t*)r, (const bf16_t*)w, (bf16_t*)h, (bf16_t*)y, rstd, rows,
+                          dim, eps)));
+  LH_CHECK_LAUNCH();
+  return LH_OK;
+}
+
+extern "C" int lh_rmsnorm_bwd(const void* dy, const void* x, const void* w, const float* rstd, const void* dres,
+                              void* dx, void* dw, float* dw_part, int parts, int64_t rows, int dim, void* stream) {
   if (!dy || !x || !w || !rstd || !dx || !dw || !dw_part || rows <= 0 || dim <= 0 || parts <= 0)
     return LH_ERR_INVALID_ARG;
-  if (!al16(dy) || !al16(x) || !al16(w) || !al16(dx)) return LH_ERR_INVALID_ARG;
+  if (!al16(dy) || !al16(x) || !al16(w) || !al16(dx) || (dres && !al16(dres))) return LH_ERR_INVALID_ARG;
   if (dim % 8 || dim > 4096) return LH_ERR_UNSUPPORTED;
   const int nc = (dim + 511) / 512;
   const int64_t rpb = (rows + parts - 1) / parts;
   const int used = (int)((rows + rpb - 1) / rpb);  // blocks that own at least one row
   LH_NC_DISPATCH(nc, (rmsnorm_bwd_kernel<NC><<<used, 256, 0, (hipStream_t)stream>>>(
-                          (const bf16_t*)dy, (const bf16_t*)x, (const bf16_t*)w, rstd, (bf16_t*)dx, dw_part,
-                          rows, dim, rpb)));
+                          (const bf16_t*)dy, (const bf16_t*)x, (const bf16_t*)w, rstd, (const bf16_t*)dres,
+                          (bf16_t*)dx, dw_part, rows, dim, rpb)));
   LH_CHECK_LAUNCH();
   rmsnorm_dw_kernel<<<(dim + 3) / 4, 256, 0, (hipStream_t)stream>>>(dw_part, (bf16_t*)dw, used, dim);
   LH_CHECK_LAUNCH();

@@ -305,6 +305,10 @@ class Attention(nn.Module):
         return ops.linear(out, self.wo.weight)
 
 
+def _eps(norm: nn.RMSNorm, x: torch.Tensor) -> float:
+    return norm.eps if norm.eps is not None else torch.finfo(x.dtype).eps
+
+
 def ffn_hidden_dim(hidden_dim: int, multiple_of: int, ffn_dim_multiplier: float | None) -> int:
     """torchtitan ``FeedForward`` width: ``int(2*h/3)``, times the multiplier, rounded
     up to ``multiple_of``.  The patch passes ``hidden_dim`` through this rule
@@ -352,8 +356,17 @@ class TransformerBlock(nn.Module):
             self.weight_init_std = 0.02 / (2 * args.n_layers) ** 0.5
 
     def forward(self, x, freqs_cis, attention_masks=None):
-        h = x + self.attention(self.attention_norm(x), freqs_cis, attention_masks)
-        return h + self.feed_forward(self.ffn_norm(h))
+        a = self.attention(self.attention_norm(x), freqs_cis, attention_masks)
+        h, y = ops.add_rms_norm(x, a, self.ffn_norm.weight, _eps(self.ffn_norm, x))
+        return h + self.feed_forward(y)
+
+    def forward_fused(self, h, y, freqs_cis, next_norm, attention_masks=None):
+        """The block on a residual stream ``h`` whose ``attention_norm(h)`` is already
+        ``y``; returns ``(h_out, next_norm(h_out))`` with both residual adds fused
+        into the norms that read them."""
+        a = self.attention(y, freqs_cis, attention_masks)
+        h, y2 = ops.add_rms_norm(h, a, self.ffn_norm.weight, _eps(self.ffn_norm, h))
+        return ops.add_rms_norm(h, self.feed_forward(y2), next_norm.weight, _eps(next_norm, h))
 
     def init_weights(self):
         for norm in (self.attention_norm, self.ffn_norm):
@@ -403,9 +416,16 @@ class Transformer(nn.Module):
 
     def forward(self, tokens: torch.Tensor, attention_masks=None):
         h = self.tok_embeddings(tokens)
-        for layer in self.layers.values():
-            h = layer(h, self.freqs_cis, attention_masks)
-        return ops.linear(self.norm(h), self.output.weight)
+        blocks = list(self.layers.values())
+        if not blocks:
+            return ops.linear(self.norm(h), self.output.weight)
+        # each residual add runs inside the RMSNorm that reads its result (the next
+        # block's attention_norm, or the final norm)
+        y = blocks[0].attention_norm(h)
+        for i, layer in enumerate(blocks):
+            nxt = blocks[i + 1].attention_norm if i + 1 < len(blocks) else self.norm
+            h, y = layer.forward_fused(h, y, self.freqs_cis, nxt, attention_masks)
+        return ops.linear(y, self.output.weight)
 
 
 def cast_params_(model: nn.Module, dtype: torch.dtype) -> nn.Module:

@@ -83,7 +83,8 @@ def test_host_validation_rejects_before_launch(pkg):
     assert lib.lh_rope_qkv_fwd(null, 3072, null, null, null, null, 1, 16, 8, 8, 128, null) == 1
     assert lib.lh_rope_qkv_bwd(null, null, null, null, null, null, 3072, 1, 16, 8, 8, 128, null) == 1
     assert lib.lh_rmsnorm_fwd(null, null, null, null, 16, 1024, ctypes.c_float(1e-5), null) == 1
-    assert lib.lh_rmsnorm_bwd(null, null, null, null, null, null, null, 4, 16, 1024, null) == 1
+    assert lib.lh_rmsnorm_bwd(null, null, null, null, null, null, null, null, 4, 16, 1024, null) == 1
+    assert lib.lh_add_rmsnorm_fwd(null, null, null, null, null, null, 16, 1024, ctypes.c_float(1e-5), null) == 1
     assert lib.lh_swiglu_fwd(null, null, 16, 1024, null) == 1
     assert lib.lh_swiglu_bwd(null, null, null, 16, 1000, null) == 1
     assert lib.lh_splitk_sum(null, null, 4, 1024, null) == 1

@@ -93,6 +93,32 @@ def test_rmsnorm(pkg, dev, rows, dim):
     assert_close(wd.grad, wr.grad, "rmsnorm dw", max_abs=1e-2, rel_l2=4e-3)
 
 
+@pytest.mark.parametrize("rows,dim", [(1000, 1024), (50, 264)])
+def test_add_rmsnorm(pkg, dev, rows, dim):
+    """h = x + r exactly as torch's bf16 add; y = RMSNorm(h); gradients with both
+    the residual branch (dh) and the normalised branch (dy) against fp64."""
+    ops = pkg.block_ops
+    g = torch.Generator().manual_seed(rows + 7)
+    x = torch.randn(rows, dim, generator=g).bfloat16()
+    r = torch.randn(rows, dim, generator=g).bfloat16()
+    w = (1 + 0.1 * torch.randn(dim, generator=g)).bfloat16()
+    xd, rd, wd = (t.to(dev).requires_grad_() for t in (x, r, w))
+    h, y = ops.add_rms_norm(xd, rd, wd, 1e-5)
+    assert torch.equal(h, x.to(dev) + r.to(dev))
+    hr = (x.double() + r.double()).bfloat16().double().requires_grad_()  # the rounded sum, as h
+    wr = w.double().requires_grad_()
+    yr = F.rms_norm(hr, (dim,), wr, 1e-5)
+    d = _ulp_diff(y, yr.bfloat16())
+    assert d.max().item() <= 1 and (d == 0).float().mean().item() >= 0.98
+    dh = torch.randn(rows, dim, generator=g).bfloat16()
+    dy = torch.randn(rows, dim, generator=g).bfloat16()
+    torch.autograd.backward([h, y], [dh.to(dev), dy.to(dev)])
+    torch.autograd.backward([hr, yr], [dh.double(), dy.double()])
+    assert_close(xd.grad, hr.grad, "add_rmsnorm dx", max_abs=1e-2, rel_l2=4e-3)
+    assert torch.equal(xd.grad, rd.grad)
+    assert_close(wd.grad, wr.grad, "add_rmsnorm dw", max_abs=1e-2, rel_l2=4e-3)
+
+
 @pytest.mark.parametrize("rows,Fh", [(777, 1024), (64, 8)])
 def test_swiglu_matches_torch_bf16_ops(pkg, dev, rows, Fh):
     """Same roundings as torch's separate bf16 silu and mul (and their backward)."""
