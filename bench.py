@@ -253,6 +253,11 @@ def run_model(args, pkg, torch):
     S_sel = pkg._native.geometry(S, wl["L"], wl["p"], wl["topk"], wl["strict"])[3]
     work = algorithmic_work(dict(wl, B=B), S_sel)
     H = margs.n_heads
+    if wl["scorer"] == "norm":
+        # the model's norm-scorer layers rotate q and k inside the pyramid pass,
+        # which also writes the rotated rows (read by the attention gathers)
+        kind, amount = work["pyramid"]
+        work["pyramid"] = (kind, amount + 2 * S * H * D * 2 * B)
     dense_pairs = S * (S + 1) / 2 * B * H
     work["dense_attn_fwd"] = ("flop", 4 * D * dense_pairs)
     work["dense_attn_bwd"] = ("flop", 10 * D * dense_pairs)   # dK/dV (4 products) + dQ (1), as in the layer

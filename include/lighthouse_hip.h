@@ -79,6 +79,31 @@ int lh_pyramid_fwd(const void *xq, const void *xk, const void *xv,
                    int base_scores_given, void *stream);
 
 /*
+ * Rotary embedding fused into the norm-scorer pyramid pass.
+ * Replaces torchtitan's apply_rotary_emb on q and k (the caller of
+ * selection_attn, lighthouse-attention.patch:707-712) followed by
+ * DialatedLighthouseNormScorer.forward (src/lighthouse_selection.py:589-616):
+ * the rows are read once, unrotated.
+ *   xq, xk, xv      bf16 rows of the q/k/v projections (q, k unrotated), strides
+ *                   (sb, ss, sh), D contiguous; e.g. column blocks of the fused
+ *                   [q | k | v] projection output
+ *   freqs           fp32 [>= S, D/2, 2] (cos, sin) per position and pair
+ *   rq, rk          bf16 rotated q, k base rows written here, strides (rb, rs, rh);
+ *                   every row is rounded to bf16 once, and the scores and pooled
+ *                   rows are those of the rounded rows (the same bits as rotating
+ *                   first and then calling lh_pyramid_fwd)
+ *   the rest as lh_pyramid_fwd with base_scores_given = 0
+ */
+int lh_rope_pyramid_fwd(const void *xq, const void *xk, const void *xv,
+                        int64_t sb, int64_t ss, int64_t sh,
+                        const float *freqs,
+                        void *rq, void *rk, int64_t rb, int64_t rs, int64_t rh,
+                        void *pq, void *pk, void *pv,
+                        int64_t pb, int64_t ps, int64_t ph,
+                        float *scores_qk, float *scores_kq,
+                        int B, int S, int H, int D, int L, int p, void *stream);
+
+/*
  * Dilated scorer base scores: ||causal_attn(q,k,v)||_2 and ||causal_attn(k,q,v)||_2
  * over the dilated virtual heads, written to scores_qk/_kq[:, :, 0:S].
  * Replaces the two SDPA calls and norms of DilatedLighthouseScorer.forward
@@ -192,6 +217,20 @@ int lh_pyramid_bwd(const void *gq, const void *gk, const void *gv,
                    const int32_t *inverse,
                    void *dxq, void *dxk, void *dxv,
                    int B, int S, int H, int D, int L, int p, void *stream);
+
+/*
+ * Pyramid backward with the rotary embedding's backward fused in: as
+ * lh_pyramid_bwd, then dxq and dxk are rotated by -theta (the adjoint of the
+ * forward rotation; torchtitan apply_rotary_emb's autograd) in fp32 before the
+ * one rounding.  Outputs have strides (ob, os, oh) in elements, D contiguous;
+ * e.g. the column blocks of the [q | k | v] projection-output gradient.
+ *   freqs   fp32 [>= S, D/2, 2], as in lh_rope_pyramid_fwd
+ */
+int lh_pyramid_rope_bwd(const void *gq, const void *gk, const void *gv,
+                        int64_t gb, int64_t gh, int64_t gs,
+                        const int32_t *inverse, const float *freqs,
+                        void *dxq, void *dxk, void *dxv, int64_t ob, int64_t os, int64_t oh,
+                        int B, int S, int H, int D, int L, int p, void *stream);
 
 /*
  * Transformer-block kernels of the Llama3 model that hosts the layer

@@ -52,6 +52,10 @@ _SIGS = {
     "lh_scatter_fwd": (_I, [_P, _P, _P, _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_scatter_bwd": (_I, [_P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_pyramid_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_rope_pyramid_fwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L,
+                                 _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_pyramid_rope_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _P, _P, _L, _L, _L,
+                                 _I, _I, _I, _I, _I, _I, _P]),
     "lh_rope_qkv_fwd": (_I, [_P, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "lh_rope_qkv_bwd": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P]),
     "lh_rmsnorm_fwd": (_I, [_P, _P, _P, _P, _L, _I, _F, _P]),
@@ -172,6 +176,43 @@ def pyramid_fwd(xq, xk, xv, L: int, p: int, scores=None, pooled_out=None):
                                   pb, ps, ph, _ptr(sqk), _ptr(skq), B, S, H, D, L, p, given, _stream(dev))
     _check(rc, "lh_pyramid_fwd")
     return pq, pk, pv, sqk, skq
+
+
+def _check_freqs(freqs, S: int, D: int):
+    assert freqs.dtype == torch.float32 and freqs.is_contiguous() and tuple(freqs.shape[1:]) == (D // 2, 2) \
+        and freqs.shape[0] >= S, "freqs must be fp32 [>= S, D/2, 2] contiguous"
+
+
+def rope_pyramid_fwd(xqkv, freqs, H: int, L: int, p: int, D: int = D_SUPPORTED):
+    """Rotary embedding fused into the pyramid pass.
+
+    ``xqkv`` bf16 [B, S, 3*H*D]: the fused [q | k | v] projection output (row
+    stride may exceed the width; D contiguous), q and k unrotated.  Returns
+    ``(xr, pq, pk, pv, scores_qk, scores_kq)``: ``xr`` [B, S, 3*H*D] with the
+    rotated q and k rows in its first two column blocks (the third block is left
+    unwritten; v rows are read from ``xqkv``), so q, k (from ``xr``) and v (from
+    ``xqkv``) share one set of strides; the rest as ``pyramid_fwd``."""
+    _need_gpu(xqkv, freqs)
+    B, S, W = xqkv.shape
+    assert W == 3 * H * D and xqkv.dtype == torch.bfloat16, "xqkv must hold [q | k | v] bf16 heads"
+    assert xqkv.stride(2) == 1 and xqkv.stride(0) == S * xqkv.stride(1), "rows of xqkv must be evenly strided"
+    _check_freqs(freqs, S, D)
+    lens, offs, S_tot = pyramid_lengths(S, L, p)
+    dev = xqkv.device
+    xr = torch.empty_strided(xqkv.shape, xqkv.stride(), dtype=torch.bfloat16, device=dev)
+    pq, pk, pv = (torch.empty(B, S_tot - S, H, D, dtype=torch.bfloat16, device=dev) for _ in range(3))
+    sqk = torch.empty(B, H, S_tot, dtype=torch.float32, device=dev)
+    skq = torch.empty_like(sqk)
+    rs = xqkv.stride(1)
+    base = xqkv.data_ptr()
+    e = xqkv.element_size()
+    with torch.cuda.device(dev):
+        rc = lib().lh_rope_pyramid_fwd(base, base + H * D * e, base + 2 * H * D * e, S * rs, rs, D,
+                                       _ptr(freqs), xr.data_ptr(), xr.data_ptr() + H * D * e, S * rs, rs, D,
+                                       _ptr(pq), _ptr(pk), _ptr(pv), *pq.stride()[:3], _ptr(sqk), _ptr(skq),
+                                       B, S, H, D, L, p, _stream(dev))
+    _check(rc, "lh_rope_pyramid_fwd")
+    return xr, pq, pk, pv, sqk, skq
 
 
 def dilated_scores(xq, xk, xv, dilation: int, S_tot: int):
@@ -361,6 +402,27 @@ def pyramid_bwd(gq, gk, gv, inverse, B: int, S: int, H: int, L: int, p: int, D: 
                                   _ptr(outs[0]), _ptr(outs[1]), _ptr(outs[2]), B, S, H, D, L, p, _stream(dev))
     _check(rc, "lh_pyramid_bwd")
     return tuple(outs)
+
+
+def pyramid_rope_bwd(gq, gk, gv, inverse, freqs, B: int, S: int, H: int, L: int, p: int, D: int = D_SUPPORTED):
+    """``pyramid_bwd`` with the rotary embedding's backward fused in: returns the
+    gradient of the fused projection output, bf16 [B, S, 3*H*D] ([dq | dk | dv],
+    dq and dk rotated back by -theta)."""
+    _need_gpu(gq, gk, gv)
+    _check_freqs(freqs, S, D)
+    gb, gh, gs, _ = gq.stride()
+    for g in (gk, gv):
+        assert tuple(g.stride()) == (gb, gh, gs, 1), "selected grads must share strides"
+    dev = gq.device
+    W = 3 * H * D
+    dx = torch.empty(B, S, W, dtype=torch.bfloat16, device=dev)
+    base, e = dx.data_ptr(), dx.element_size()
+    with torch.cuda.device(dev):
+        rc = lib().lh_pyramid_rope_bwd(_ptr(gq), _ptr(gk), _ptr(gv), gb, gh, gs, _ptr(inverse), _ptr(freqs),
+                                       base, base + H * D * e, base + 2 * H * D * e, S * W, W, D,
+                                       B, S, H, D, L, p, _stream(dev))
+    _check(rc, "lh_pyramid_rope_bwd")
+    return dx
 
 
 # ---------------------------------------------------------------------------

@@ -48,6 +48,39 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 }
 
 // ---------------------------------------------------------------------------
+// Rotary embedding of 8 consecutive elements of a row (pairs j = 0..3 are
+// (f[2j], f[2j+1])) by the angles whose (cos, sin) pairs are c01 = (c0, s0, c1, s1)
+// and c23 = (c2, s2, c3, s3).  FWD rotates by +theta (torchtitan's
+// apply_rotary_emb: the complex product x * e^{i theta}), otherwise by -theta
+// (its adjoint).  The fma placement is fixed here so every kernel that rotates
+// produces the same bits.
+// ---------------------------------------------------------------------------
+template <bool FWD>
+__device__ __forceinline__ void rope_rotate8(float* f, const float4 c01, const float4 c23) {
+  const float c[4] = {c01.x, c01.z, c23.x, c23.z};
+  const float s[4] = {c01.y, c01.w, c23.y, c23.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float x0 = f[2 * j], x1 = f[2 * j + 1];
+    if (FWD) {
+      f[2 * j] = fmaf(x0, c[j], -(x1 * s[j]));
+      f[2 * j + 1] = fmaf(x0, s[j], x1 * c[j]);
+    } else {
+      f[2 * j] = fmaf(x0, c[j], x1 * s[j]);
+      f[2 * j + 1] = fmaf(x1, c[j], -(x0 * s[j]));
+    }
+  }
+}
+
+// (cos, sin) of the 4 pairs starting at element d0 (a multiple of 8) of position t,
+// from a [.., D/2, 2] fp32 table
+__device__ __forceinline__ void rope_freqs8(const float* fs, int64_t t, int D, int d0, float4& c01, float4& c23) {
+  const float4* cs = reinterpret_cast<const float4*>(fs + (t * (D / 2) + d0 / 2) * 2);
+  c01 = cs[0];
+  c23 = cs[1];
+}
+
+// ---------------------------------------------------------------------------
 // pyramid geometry (integer forms)
 // ---------------------------------------------------------------------------
 // Level l (1-based) has S / p^(l-1) nodes; levels are concatenated base first.

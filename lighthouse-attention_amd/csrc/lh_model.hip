@@ -59,21 +59,9 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(const RopeArgs a) {
   if (which < 2) {
     float f[kVec];
     unpack8(in, f);
-    const float4* cs = reinterpret_cast<const float4*>(a.fs + ((int64_t)t * (a.D / 2) + d0 / 2) * 2);
-    const float4 c01 = cs[0], c23 = cs[1];  // (cos, sin) of pairs j..j+3
-    const float cj[4] = {c01.x, c01.z, c23.x, c23.z};
-    const float sj[4] = {c01.y, c01.w, c23.y, c23.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float x0 = f[2 * j], x1 = f[2 * j + 1];
-      if (FWD) {
-        f[2 * j] = x0 * cj[j] - x1 * sj[j];
-        f[2 * j + 1] = x0 * sj[j] + x1 * cj[j];
-      } else {
-        f[2 * j] = x0 * cj[j] + x1 * sj[j];
-        f[2 * j + 1] = x1 * cj[j] - x0 * sj[j];
-      }
-    }
+    float4 c01, c23;
+    rope_freqs8(a.fs, t, a.D, d0, c01, c23);
+    rope_rotate8<FWD>(f, c01, c23);
     o = pack8(f);
   }
   if (FWD) {

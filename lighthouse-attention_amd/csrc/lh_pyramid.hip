@@ -23,13 +23,20 @@ struct PyrArgs {
   bf16_t *pq, *pk, *pv;
   int64_t pb, ps, ph;
   float *sqk, *skq;
+  const float* fs;   // rotary (cos, sin) table [>= S, D/2, 2] (ROPE)
+  bf16_t *rq, *rk;   // rotated base rows out (ROPE)
+  int64_t rb, rs, rh;
   int B, S, H, L, shift, S_tot, nspan, cmax, units;
   int off[9];
 };
 
 __device__ __forceinline__ uint4 ld16(const bf16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
-template <int NL, bool GIVEN>
+// ROPE: xq / xk are the projection's unrotated rows; each is rotated by its
+// position's angles, rounded to bf16 and written to rq / rk, and the norms and
+// means below are taken of those rounded rows, exactly as if the rotated rows
+// had been stored first and read back.
+template <int NL, bool GIVEN, bool ROPE>
 __global__ __launch_bounds__(256) void pyramid_fwd_kernel(const PyrArgs a) {
   const int tid = threadIdx.x;
   const int u = blockIdx.x * 16 + (tid >> 4);
@@ -58,6 +65,18 @@ __global__ __launch_bounds__(256) void pyramid_fwd_kernel(const PyrArgs a) {
     unpack8(ld16(a.xq + o), fq);
     unpack8(ld16(a.xk + o), fk);
     unpack8(ld16(a.xv + o), fv);
+    if (ROPE) {
+      float4 c01, c23;
+      rope_freqs8(a.fs, t, LH_D, 8 * l16, c01, c23);
+      rope_rotate8<true>(fq, c01, c23);
+      rope_rotate8<true>(fk, c01, c23);
+      const uint4 wq = pack8(fq), wk = pack8(fk);
+      const int64_t ro = (int64_t)b * a.rb + (int64_t)t * a.rs + (int64_t)h * a.rh + 8 * l16;
+      *reinterpret_cast<uint4*>(a.rq + ro) = wq;
+      *reinterpret_cast<uint4*>(a.rk + ro) = wk;
+      unpack8(wq, fq);
+      unpack8(wk, fk);
+    }
     float sq, sk;
     if (GIVEN) {
       sq = a.sqk[srow + t];
@@ -111,6 +130,8 @@ struct PyrBwdArgs {
   int64_t gb, gh, gs;
   const int32_t* inv;
   bf16_t *dq, *dk, *dv;
+  int64_t ob, os, oh;  // strides of the three outputs (element units)
+  const float* fs;     // ROPE: (cos, sin) table; dq, dk are rotated back by -theta
   int B, S, H, L, shift, S_tot;
   int off[9], len[9];
   long long rows;
@@ -118,8 +139,10 @@ struct PyrBwdArgs {
 
 // One 16-lane group per (b, t, h) row, 8 d each.  All levels' inverse lookups
 // are issued first, then all gradient-row loads, so a row costs two dependent
-// memory round trips instead of two per level.
-template <int NL>
+// memory round trips instead of two per level.  ROPE: the q and k sums are
+// the gradients of rotated rows; they are rotated back (the adjoint of the
+// forward rotation) in fp32 before the one rounding.
+template <int NL, bool ROPE>
 __global__ __launch_bounds__(256) void pyramid_bwd_kernel(const PyrBwdArgs a) {
   const int tid = threadIdx.x;
   const long long row = (long long)blockIdx.x * 16 + (tid >> 4);
@@ -162,7 +185,13 @@ __global__ __launch_bounds__(256) void pyramid_bwd_kernel(const PyrBwdArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) fv[e] = fmaf(g[e], w, fv[e]);
   }
-  const size_t o = (size_t)row * LH_D + 8 * l16;
+  if (ROPE) {
+    float4 c01, c23;
+    rope_freqs8(a.fs, t, LH_D, 8 * l16, c01, c23);
+    rope_rotate8<false>(fq, c01, c23);
+    rope_rotate8<false>(fk, c01, c23);
+  }
+  const int64_t o = (int64_t)b * a.ob + (int64_t)t * a.os + (int64_t)h * a.oh + 8 * l16;
   if (a.dq) *reinterpret_cast<uint4*>(a.dq + o) = pack8(fq);
   if (a.dk) *reinterpret_cast<uint4*>(a.dk + o) = pack8(fk);
   if (a.dv) *reinterpret_cast<uint4*>(a.dv + o) = pack8(fv);
@@ -171,10 +200,12 @@ __global__ __launch_bounds__(256) void pyramid_bwd_kernel(const PyrBwdArgs a) {
 template <int NL>
 int launch_fwd(const PyrArgs& a, bool given, hipStream_t st) {
   const int blocks = (a.units + 15) / 16;
-  if (given)
-    hipLaunchKernelGGL((pyramid_fwd_kernel<NL, true>), dim3(blocks), dim3(256), 0, st, a);
+  if (a.fs)
+    hipLaunchKernelGGL((pyramid_fwd_kernel<NL, false, true>), dim3(blocks), dim3(256), 0, st, a);
+  else if (given)
+    hipLaunchKernelGGL((pyramid_fwd_kernel<NL, true, false>), dim3(blocks), dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((pyramid_fwd_kernel<NL, false>), dim3(blocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((pyramid_fwd_kernel<NL, false, false>), dim3(blocks), dim3(256), 0, st, a);
   LH_CHECK_LAUNCH();
   return LH_OK;
 }
@@ -183,10 +214,13 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 }  // namespace
 
-extern "C" int lh_pyramid_fwd(const void* xq, const void* xk, const void* xv, int64_t sb, int64_t ss, int64_t sh,
-                              void* pq, void* pk, void* pv, int64_t pb, int64_t ps, int64_t ph,
-                              float* scores_qk, float* scores_kq, int B, int S, int H, int D, int L, int p,
-                              int base_scores_given, void* stream) {
+namespace {
+
+int pyramid_fwd_impl(const void* xq, const void* xk, const void* xv, int64_t sb, int64_t ss, int64_t sh,
+                     const float* freqs, void* rq, void* rk, int64_t rb, int64_t rs, int64_t rh,
+                     void* pq, void* pk, void* pv, int64_t pb, int64_t ps, int64_t ph,
+                     float* scores_qk, float* scores_kq, int B, int S, int H, int D, int L, int p,
+                     bool given, void* stream) {
   if (D != LH_D) return LH_ERR_UNSUPPORTED;
   if (!xq || !xk || !xv || !scores_qk || !scores_kq || B <= 0 || H <= 0 || S <= 0) return LH_ERR_INVALID_ARG;
   const int shift = ilog2_exact(p);
@@ -196,6 +230,8 @@ extern "C" int lh_pyramid_fwd(const void* xq, const void* xk, const void* xv, in
   if ((sb | ss | sh) % 8 || (L > 1 && (pb | ps | ph) % 8)) return LH_ERR_INVALID_ARG;
   if (!aligned16(xq) || !aligned16(xk) || !aligned16(xv) || (L > 1 && (!aligned16(pq) || !aligned16(pk) || !aligned16(pv))))
     return LH_ERR_INVALID_ARG;
+  if (freqs && (!rq || !rk || !aligned16(freqs) || !aligned16(rq) || !aligned16(rk) || (rb | rs | rh) % 8))
+    return LH_ERR_INVALID_ARG;
   Pyramid g;
   if (!make_pyramid(S, L, p, &g)) return LH_ERR_INVALID_ARG;
   PyrArgs a{};
@@ -204,6 +240,8 @@ extern "C" int lh_pyramid_fwd(const void* xq, const void* xk, const void* xv, in
   a.pq = (bf16_t*)pq; a.pk = (bf16_t*)pk; a.pv = (bf16_t*)pv;
   a.pb = pb; a.ps = ps; a.ph = ph;
   a.sqk = scores_qk; a.skq = scores_kq;
+  a.fs = freqs; a.rq = (bf16_t*)rq; a.rk = (bf16_t*)rk;
+  a.rb = rb; a.rs = rs; a.rh = rh;
   a.B = B; a.S = S; a.H = H; a.L = L; a.shift = shift; a.S_tot = g.total;
   a.cmax = ipow(p, L - 1);
   if (a.cmax > 4096) return LH_ERR_UNSUPPORTED;
@@ -213,7 +251,6 @@ extern "C" int lh_pyramid_fwd(const void* xq, const void* xk, const void* xv, in
   a.units = (int)units;
   for (int l = 1; l <= L; ++l) a.off[l] = g.off[l];
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const bool given = base_scores_given != 0;
   switch (L - 1) {
     case 0: return launch_fwd<0>(a, given, st);
     case 1: return launch_fwd<1>(a, given, st);
@@ -224,39 +261,88 @@ extern "C" int lh_pyramid_fwd(const void* xq, const void* xk, const void* xv, in
   }
 }
 
-extern "C" int lh_pyramid_bwd(const void* gq, const void* gk, const void* gv, int64_t gb, int64_t gh, int64_t gs,
-                              const int32_t* inverse, void* dxq, void* dxk, void* dxv, int B, int S, int H, int D,
-                              int L, int p, void* stream) {
+template <bool ROPE>
+void launch_bwd(const PyrBwdArgs& a, dim3 grid, hipStream_t st) {
+  const dim3 blk(256);
+  switch (a.L) {
+    case 1: hipLaunchKernelGGL((pyramid_bwd_kernel<1, ROPE>), grid, blk, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((pyramid_bwd_kernel<2, ROPE>), grid, blk, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((pyramid_bwd_kernel<3, ROPE>), grid, blk, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((pyramid_bwd_kernel<4, ROPE>), grid, blk, 0, st, a); break;
+    case 5: hipLaunchKernelGGL((pyramid_bwd_kernel<5, ROPE>), grid, blk, 0, st, a); break;
+    case 6: hipLaunchKernelGGL((pyramid_bwd_kernel<6, ROPE>), grid, blk, 0, st, a); break;
+    case 7: hipLaunchKernelGGL((pyramid_bwd_kernel<7, ROPE>), grid, blk, 0, st, a); break;
+    default: hipLaunchKernelGGL((pyramid_bwd_kernel<8, ROPE>), grid, blk, 0, st, a); break;
+  }
+}
+
+int pyramid_bwd_impl(const void* gq, const void* gk, const void* gv, int64_t gb, int64_t gh, int64_t gs,
+                     const int32_t* inverse, const float* freqs, void* dxq, void* dxk, void* dxv, int64_t ob,
+                     int64_t os, int64_t oh, int B, int S, int H, int D, int L, int p, void* stream) {
   if (D != LH_D) return LH_ERR_UNSUPPORTED;
   if (B <= 0 || H <= 0 || S <= 0 || L < 1 || L > 8) return LH_ERR_INVALID_ARG;
   const int shift = ilog2_exact(p);
   if (shift <= 0) return LH_ERR_INVALID_ARG;
   if ((gq != nullptr) != (dxq != nullptr) || (gk != nullptr) != (dxk != nullptr) || (gv != nullptr) != (dxv != nullptr))
     return LH_ERR_INVALID_ARG;
-  if ((gb | gh | gs) % 8) return LH_ERR_INVALID_ARG;
+  if ((gb | gh | gs) % 8 || (ob | os | oh) % 8) return LH_ERR_INVALID_ARG;
+  for (const void* x : {gq, gk, gv, (const void*)dxq, (const void*)dxk, (const void*)dxv})
+    if (x && !aligned16(x)) return LH_ERR_INVALID_ARG;
+  if (freqs && !aligned16(freqs)) return LH_ERR_INVALID_ARG;
   Pyramid g;
   if (!make_pyramid(S, L, p, &g)) return LH_ERR_INVALID_ARG;
   PyrBwdArgs a{};
   a.gq = (const bf16_t*)gq; a.gk = (const bf16_t*)gk; a.gv = (const bf16_t*)gv;
   a.gb = gb; a.gh = gh; a.gs = gs; a.inv = inverse;
   a.dq = (bf16_t*)dxq; a.dk = (bf16_t*)dxk; a.dv = (bf16_t*)dxv;
+  a.ob = ob; a.os = os; a.oh = oh; a.fs = freqs;
   a.B = B; a.S = S; a.H = H; a.L = L; a.shift = shift; a.S_tot = g.total;
   for (int l = 1; l <= L; ++l) { a.off[l] = g.off[l]; a.len[l] = g.len[l]; }
   a.rows = (long long)B * S * H;
   const long long blocks = (a.rows + 15) / 16;
   if (blocks > 2147483647LL) return LH_ERR_UNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)blocks), blk(256);
-  switch (L) {
-    case 1: hipLaunchKernelGGL(pyramid_bwd_kernel<1>, grid, blk, 0, st, a); break;
-    case 2: hipLaunchKernelGGL(pyramid_bwd_kernel<2>, grid, blk, 0, st, a); break;
-    case 3: hipLaunchKernelGGL(pyramid_bwd_kernel<3>, grid, blk, 0, st, a); break;
-    case 4: hipLaunchKernelGGL(pyramid_bwd_kernel<4>, grid, blk, 0, st, a); break;
-    case 5: hipLaunchKernelGGL(pyramid_bwd_kernel<5>, grid, blk, 0, st, a); break;
-    case 6: hipLaunchKernelGGL(pyramid_bwd_kernel<6>, grid, blk, 0, st, a); break;
-    case 7: hipLaunchKernelGGL(pyramid_bwd_kernel<7>, grid, blk, 0, st, a); break;
-    default: hipLaunchKernelGGL(pyramid_bwd_kernel<8>, grid, blk, 0, st, a); break;
-  }
+  if (freqs)
+    launch_bwd<true>(a, dim3((unsigned)blocks), st);
+  else
+    launch_bwd<false>(a, dim3((unsigned)blocks), st);
   LH_CHECK_LAUNCH();
   return LH_OK;
+}
+
+}  // namespace
+
+extern "C" int lh_pyramid_fwd(const void* xq, const void* xk, const void* xv, int64_t sb, int64_t ss, int64_t sh,
+                              void* pq, void* pk, void* pv, int64_t pb, int64_t ps, int64_t ph,
+                              float* scores_qk, float* scores_kq, int B, int S, int H, int D, int L, int p,
+                              int base_scores_given, void* stream) {
+  return pyramid_fwd_impl(xq, xk, xv, sb, ss, sh, nullptr, nullptr, nullptr, 0, 0, 0, pq, pk, pv, pb, ps, ph,
+                          scores_qk, scores_kq, B, S, H, D, L, p, base_scores_given != 0, stream);
+}
+
+extern "C" int lh_rope_pyramid_fwd(const void* xq, const void* xk, const void* xv, int64_t sb, int64_t ss,
+                                   int64_t sh, const float* freqs, void* rq, void* rk, int64_t rb, int64_t rs,
+                                   int64_t rh, void* pq, void* pk, void* pv, int64_t pb, int64_t ps, int64_t ph,
+                                   float* scores_qk, float* scores_kq, int B, int S, int H, int D, int L, int p,
+                                   void* stream) {
+  if (!freqs) return LH_ERR_INVALID_ARG;
+  return pyramid_fwd_impl(xq, xk, xv, sb, ss, sh, freqs, rq, rk, rb, rs, rh, pq, pk, pv, pb, ps, ph, scores_qk,
+                          scores_kq, B, S, H, D, L, p, false, stream);
+}
+
+extern "C" int lh_pyramid_bwd(const void* gq, const void* gk, const void* gv, int64_t gb, int64_t gh, int64_t gs,
+                              const int32_t* inverse, void* dxq, void* dxk, void* dxv, int B, int S, int H, int D,
+                              int L, int p, void* stream) {
+  const int64_t oh = D, os = (int64_t)H * D, ob = (int64_t)S * os;
+  return pyramid_bwd_impl(gq, gk, gv, gb, gh, gs, inverse, nullptr, dxq, dxk, dxv, ob, os, oh, B, S, H, D, L, p,
+                          stream);
+}
+
+extern "C" int lh_pyramid_rope_bwd(const void* gq, const void* gk, const void* gv, int64_t gb, int64_t gh,
+                                   int64_t gs, const int32_t* inverse, const float* freqs, void* dxq, void* dxk,
+                                   void* dxv, int64_t ob, int64_t os, int64_t oh, int B, int S, int H, int D, int L,
+                                   int p, void* stream) {
+  if (!freqs) return LH_ERR_INVALID_ARG;
+  return pyramid_bwd_impl(gq, gk, gv, gb, gh, gs, inverse, freqs, dxq, dxk, dxv, ob, os, oh, B, S, H, D, L, p,
+                          stream);
 }

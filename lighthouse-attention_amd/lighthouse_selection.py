@@ -47,7 +47,7 @@ __all__ = [
     "DilatedLighthouseScorer", "DialatedLighthouseNormScorer", "DilatedLighthouseGLAScorer",
     "LighthouseLocal", "DialatedLighthouseNormScorerCP", "LighthouseCP", "scatter_to_base_sequence",
     "LighthouseSelectionQkKqChunkedTopkNvrtc", "LighthouseSelectionQkKqChunkedTopkHip",
-    "compute_output_indices_selection", "lighthouse_layer",
+    "compute_output_indices_selection", "lighthouse_layer", "lighthouse_layer_rope",
 ]
 
 
@@ -186,6 +186,86 @@ def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, t
             raise TypeError("the native layer computes in bfloat16; got " + str(t.dtype))
     return _LighthouseLayerFn.apply(xq, xk, xv, num_levels, pooling_factor, topk, tie_break, strict,
                                     int(dilation), bool(seq_major))
+
+
+class _LighthouseRopeLayerFn(torch.autograd.Function):
+    """The layer fed straight from the fused [q | k | v] projection output: the
+    rotary embedding of q and k runs inside the pyramid pass (and its adjoint
+    inside the pyramid backward), otherwise exactly ``_LighthouseLayerFn`` with
+    the norm scorer.  The rotated rows are stored once, for the attention
+    kernels' gathers; v rows are read from the projection output in place."""
+
+    @staticmethod
+    def forward(ctx, xqkv, freqs, H, L, p, topk, tie, strict, seq_major):
+        B, S, W = xqkv.shape
+        D = W // (3 * H)
+        _, _, _, S_sel = N.geometry(S, L, p, topk, strict)
+        _mark("fwd_start")
+        xr, pq, pk, pv, sqk, skq = N.rope_pyramid_fwd(xqkv, freqs, H, L, p, D)
+        _mark("pyramid")
+        idx, inv = N.select_topk(sqk, skq, S, L, p, topk, tie=tie, strict=strict)
+        _mark("select")
+        rows = _rope_rows(xqkv, xr, H, D, pq, pk, pv)
+        o, lse = N.attn_fwd(rows, idx, B, H, S_sel, D)
+        _mark("attn_fwd")
+        out = N.scatter_fwd(o, inv, S, S, L, p, seq_major=seq_major)
+        _mark("scatter_fwd")
+        ctx.save_for_backward(xqkv, xr, freqs, pq, pk, pv, idx, inv, o, lse)
+        ctx.geo = (B, S, H, D, L, p, S_sel)
+        ctx.mark_non_differentiable(idx)
+        ctx.set_materialize_grads(False)
+        return out, idx
+
+    @staticmethod
+    def backward(ctx, dout, _didx):
+        xqkv, xr, freqs, pq, pk, pv, idx, inv, o, lse = ctx.saved_tensors
+        B, S, H, D, L, p, S_sel = ctx.geo
+        if dout is None:
+            return (None,) * 9
+        _mark("bwd_start")
+        dattn, delta = N.scatter_bwd(dout, idx, o, S, L, p)
+        _mark("scatter_bwd")
+        rows = _rope_rows(xqkv, xr, H, D, pq, pk, pv)
+        dks, dvs = N.attn_bwd_dkdv(rows, idx, B, H, S_sel, dattn, lse, delta, D)
+        _mark("attn_bwd_dkdv")
+        dqs = N.attn_bwd_dq(rows, idx, B, H, S_sel, dattn, lse, delta, D)
+        _mark("attn_bwd_dq")
+        dx = N.pyramid_rope_bwd(dqs, dks, dvs, inv, freqs, B, S, H, L, p, D)
+        _mark("pyramid_bwd")
+        return dx, None, None, None, None, None, None, None, None
+
+
+def _rope_rows(xqkv, xr, H, D, pq, pk, pv):
+    B, S, _ = xqkv.shape
+    hd = H * D
+    q, k = xr[..., :hd], xr[..., hd:2 * hd]
+    v = xqkv[..., 2 * hd:]
+    sb, ss, _ = xqkv.stride()
+    pb, ps, ph, _ = pq.stride()
+    return N.Rows(q, k, v, (sb, ss, D), pq, pk, pv, (pb, ps, ph), split=S)
+
+
+def lighthouse_layer_rope(xqkv, freqs, n_heads: int, num_levels: int = 3, pooling_factor: int = 4,
+                          topk: int = 1024, tie_break: str = "reference", strict: bool = True,
+                          seq_major: bool = False):
+    """The norm-scorer layer applied to the fused projection output.
+
+    ``xqkv`` bf16 [B, S, 3*H*D] = [q | k | v] heads before the rotary embedding;
+    ``freqs`` fp32 [>= S, D/2, 2] = (cos, sin) per position and pair (the real view
+    of torchtitan's ``freqs_cis``).  Equal to ``lighthouse_layer(rope(q), rope(k), v)``:
+    the forward gives the same bits as rotating first (rotation rounded to bf16 once
+    per element), the gradient w.r.t. ``xqkv`` is the rotated-back pyramid gradient
+    rounded once.  Returns ``(out [B, H, S, D], indices)``."""
+    B, S, W = xqkv.shape
+    if W % (3 * n_heads) or W // (3 * n_heads) != N.D_SUPPORTED:
+        raise ValueError(f"xqkv must hold 3 x {n_heads} heads of dim {N.D_SUPPORTED}, got width {W}")
+    if xqkv.dtype != torch.bfloat16:
+        raise TypeError("the native layer computes in bfloat16; got " + str(xqkv.dtype))
+    if xqkv.stride(2) != 1 or xqkv.stride(1) % 8 or xqkv.stride(0) != S * xqkv.stride(1):
+        xqkv = xqkv.contiguous()
+    freqs = freqs.contiguous()
+    return _LighthouseRopeLayerFn.apply(xqkv, freqs, n_heads, num_levels, pooling_factor, topk, tie_break, strict,
+                                        bool(seq_major))
 
 
 class _PyramidCatFn(torch.autograd.Function):
@@ -393,6 +473,22 @@ class LighthouseLocal(nn.Module):
         if type(sc) is DilatedLighthouseScorer and sc.attention is None:
             return sc.dilation
         return None
+
+    def fuses_rope(self) -> bool:
+        """True when ``forward_rope`` applies: the native path with the norm scorer."""
+        return self.use_native_attention and self._native_dilation() == 0 and \
+            self.scorer.levels == self.num_levels and self.scorer.pooling_factor == self.pooling_factor
+
+    def forward_rope(self, xqkv, freqs, n_heads: int):
+        """``forward(rope(q), rope(k), v)`` from the fused ``[q | k | v]`` projection
+        output ``xqkv`` [B, S, 3*H*D] and the rotary table ``freqs`` fp32
+        [>= S, D/2, 2]; the rotation runs inside the layer's pyramid pass."""
+        if not self.fuses_rope():
+            raise RuntimeError("forward_rope needs the native layer with the norm scorer")
+        out, idx = lighthouse_layer_rope(xqkv, freqs, n_heads, self.num_levels, self.pooling_factor, self.topk,
+                                         self.tie_break, self.strict, self.out_seq_major)
+        self.last_indices = idx
+        return out
 
     def forward(self, xq, xk, xv):
         _, s, _, d = xq.shape

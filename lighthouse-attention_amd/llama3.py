@@ -276,6 +276,10 @@ class Attention(nn.Module):
             nn.init.trunc_normal_(self.wg.weight, mean=0.0, std=0.02)
             nn.init.zeros_(self.wg.bias)
 
+    def _fuses_rope(self) -> bool:
+        return (not self._needs_gate and self.n_kv_heads == self.n_heads
+                and isinstance(self.selection_attn, LighthouseLocal) and self.selection_attn.fuses_rope())
+
     def set_use_lighthouse(self, use_lighthouse: bool):
         self._use_lighthouse = use_lighthouse
 
@@ -288,10 +292,16 @@ class Attention(nn.Module):
         # one projection GEMM for [q | k | v]; rotary embedding and the split in one pass
         wqkv = torch.cat([self.wq.weight, self.wk.weight, self.wv.weight])
         xqkv = ops.linear(x, wqkv)
-        xq, xk, xv = ops.rope_qkv(xqkv, torch.view_as_real(freqs_cis), self.n_heads, self.n_kv_heads, self.head_dim)
         if attention_masks is not None:
             raise NotImplementedError("document masks need flex attention, which is not part of this build")
-        if self.use_selection_lighthouse and self._use_lighthouse:
+        lighthouse = self.use_selection_lighthouse and self._use_lighthouse
+        if lighthouse and self._fuses_rope():
+            # the norm-scorer layer rotates q and k inside its pyramid pass
+            out = self.selection_attn.forward_rope(xqkv, torch.view_as_real(freqs_cis), self.n_heads)
+            out = out.transpose(1, 2).contiguous().view(bs, seqlen, -1)
+            return ops.linear(out, self.wo.weight)
+        xq, xk, xv = ops.rope_qkv(xqkv, torch.view_as_real(freqs_cis), self.n_heads, self.n_kv_heads, self.head_dim)
+        if lighthouse:
             if self._needs_gate:
                 gk = F.logsigmoid(self.wg(x)) / self.gate_logit_normalizer
                 out = self.selection_attn(xq, xk, xv, gk=gk)

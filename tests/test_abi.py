@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol(pkg):
     for n in _declared():
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
     assert set(_declared()) == set(pkg._native.EXPORTED)
-    assert lib.lh_abi_version() == 2
+    assert lib.lh_abi_version() == 3
 
 
 def test_strerror(pkg):
@@ -81,6 +81,17 @@ def test_host_validation_rejects_before_launch(pkg):
     assert lib.lh_select_geometry(4096, 1, 4, 256, 0, None, None, None, None) == 1
     # transformer-block kernels
     assert lib.lh_rope_qkv_fwd(null, 3072, null, null, null, null, 1, 16, 8, 8, 128, null) == 1
+    fake = ctypes.c_void_p(64)  # never dereferenced: every call below is refused first
+    assert lib.lh_rope_pyramid_fwd(null, null, null, 0, 0, 0, null, null, null, 0, 0, 0, null, null, null,
+                                   0, 0, 0, null, null, 1, 1024, 1, 128, 3, 4, null) == 1
+    assert lib.lh_rope_pyramid_fwd(null, null, null, 0, 0, 0, fake, null, null, 0, 0, 0, null, null, null,
+                                   0, 0, 0, null, null, 1, 1024, 1, 128, 3, 4, null) == 1
+    assert lib.lh_rope_pyramid_fwd(fake, fake, fake, 384, 384, 128, fake, null, fake, 384, 384, 128, fake, fake,
+                                   fake, 128, 128, 128, fake, fake, 1, 1024, 1, 128, 3, 4, null) == 1  # rq null
+    assert lib.lh_pyramid_rope_bwd(null, null, null, 0, 0, 0, null, null, null, null, null, 0, 0, 0,
+                                   1, 1024, 1, 128, 3, 4, null) == 1  # freqs null
+    assert lib.lh_pyramid_rope_bwd(fake, null, null, 8, 8, 8, null, fake, null, null, null, 8, 8, 8,
+                                   1, 1024, 1, 128, 3, 4, null) == 1  # grad without output
     assert lib.lh_rope_qkv_bwd(null, null, null, null, null, null, 3072, 1, 16, 8, 8, 128, null) == 1
     assert lib.lh_rmsnorm_fwd(null, null, null, null, 16, 1024, ctypes.c_float(1e-5), null) == 1
     assert lib.lh_rmsnorm_bwd(null, null, null, null, null, null, null, null, 4, 16, 1024, null) == 1
