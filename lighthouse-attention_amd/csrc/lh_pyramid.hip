@@ -27,10 +27,47 @@ struct PyrArgs {
   bf16_t *rq, *rk;   // rotated base rows out (ROPE)
   int64_t rb, rs, rh;
   int B, S, H, L, shift, S_tot, nspan, cmax, units;
-  int off[9];
+  int off[9], len[9];
 };
 
 __device__ __forceinline__ uint4 ld16(const bf16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+constexpr int PYR_CHUNK = 4;  // base tokens whose loads are issued together
+
+// One base token t of (b, h): unpack the 16-byte slices of its q, k, v rows,
+// rotate q and k (ROPE: rounded to bf16 and stored to rq / rk, the rounded
+// values kept), and make its base scores: the bf16-rounded L2 norms of q and k
+// (every lane of the 16-lane group gets them), or the given ones (GIVEN: sq, sk
+// on entry).
+template <bool GIVEN, bool ROPE>
+__device__ __forceinline__ void pyr_token(const PyrArgs& a, int b, int h, int l16, size_t srow, int t,
+                                          const uint4 xq, const uint4 xk, const uint4 xv, float* fq, float* fk,
+                                          float* fv, float& sq, float& sk) {
+  unpack8(xq, fq);
+  unpack8(xk, fk);
+  unpack8(xv, fv);
+  if (ROPE) {
+    float4 c01, c23;
+    rope_freqs8(a.fs, t, LH_D, 8 * l16, c01, c23);
+    rope_rotate8<true>(fq, c01, c23);
+    rope_rotate8<true>(fk, c01, c23);
+    const uint4 wq = pack8(fq), wk = pack8(fk);
+    const int64_t ro = (int64_t)b * a.rb + (int64_t)t * a.rs + (int64_t)h * a.rh + 8 * l16;
+    *reinterpret_cast<uint4*>(a.rq + ro) = wq;
+    *reinterpret_cast<uint4*>(a.rk + ro) = wk;
+    unpack8(wq, fq);
+    unpack8(wk, fk);
+  }
+  if (!GIVEN) {
+    float pq = 0.f, pk = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { pq = fmaf(fq[e], fq[e], pq); pk = fmaf(fk[e], fk[e], pk); }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) { pq += __shfl_xor(pq, m, 16); pk += __shfl_xor(pk, m, 16); }
+    sq = bf16_to_f32(f32_to_bf16(sqrtf(pq)));
+    sk = bf16_to_f32(f32_to_bf16(sqrtf(pk)));
+  }
+}
 
 // ROPE: xq / xk are the projection's unrotated rows; each is rotated by its
 // position's angles, rounded to bf16 and written to rq / rk, and the norms and
@@ -59,37 +96,21 @@ __global__ __launch_bounds__(256) void pyramid_fwd_kernel(const PyrArgs a) {
     for (int e = 0; e < 8; ++e) { accq[l][e] = 0.f; acck[l][e] = 0.f; accv[l][e] = 0.f; }
   }
   const int64_t xoff = (int64_t)b * a.sb + (int64_t)h * a.sh + 8 * l16;
-  for (int t = t0; t < t1; ++t) {
-    const int64_t o = xoff + (int64_t)t * a.ss;
+  float bq = 0.f, bk = 0.f;  // this lane's pending base scores
+  // one base token: rows (q, k, v) as loaded, base scores when GIVEN
+  auto token = [&](int t, const uint4 xq, const uint4 xk, const uint4 xv, float sq, float sk)
+      __attribute__((always_inline)) {
     float fq[8], fk[8], fv[8];
-    unpack8(ld16(a.xq + o), fq);
-    unpack8(ld16(a.xk + o), fk);
-    unpack8(ld16(a.xv + o), fv);
-    if (ROPE) {
-      float4 c01, c23;
-      rope_freqs8(a.fs, t, LH_D, 8 * l16, c01, c23);
-      rope_rotate8<true>(fq, c01, c23);
-      rope_rotate8<true>(fk, c01, c23);
-      const uint4 wq = pack8(fq), wk = pack8(fk);
-      const int64_t ro = (int64_t)b * a.rb + (int64_t)t * a.rs + (int64_t)h * a.rh + 8 * l16;
-      *reinterpret_cast<uint4*>(a.rq + ro) = wq;
-      *reinterpret_cast<uint4*>(a.rk + ro) = wk;
-      unpack8(wq, fq);
-      unpack8(wk, fk);
-    }
-    float sq, sk;
-    if (GIVEN) {
-      sq = a.sqk[srow + t];
-      sk = a.skq[srow + t];
-    } else {
-      float pq = 0.f, pk = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) { pq = fmaf(fq[e], fq[e], pq); pk = fmaf(fk[e], fk[e], pk); }
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) { pq += __shfl_xor(pq, m, 16); pk += __shfl_xor(pk, m, 16); }
-      sq = bf16_to_f32(f32_to_bf16(sqrtf(pq)));
-      sk = bf16_to_f32(f32_to_bf16(sqrtf(pk)));
-      if (l16 == 0) { a.sqk[srow + t] = sq; a.skq[srow + t] = sk; }
+    pyr_token<GIVEN, ROPE>(a, b, h, l16, srow, t, xq, xk, xv, fq, fk, fv, sq, sk);
+    if (!GIVEN) {
+      // base scores leave 16 tokens at a time: lane j keeps token t0 + 16 i + j,
+      // and the group stores them as one contiguous 64-byte run per tensor
+      const int j = (t - t0) & 15;
+      if (l16 == j) { bq = sq; bk = sk; }
+      if ((j == 15 || t == t1 - 1) && l16 <= j) {
+        a.sqk[srow + t - j + l16] = bq;
+        a.skq[srow + t - j + l16] = bk;
+      }
     }
 #pragma unroll
     for (int l = 0; l < NL; ++l) {
@@ -122,6 +143,30 @@ __global__ __launch_bounds__(256) void pyramid_fwd_kernel(const PyrArgs a) {
         mq[l] = -INFINITY; mk[l] = -INFINITY;
       }
     }
+  };
+  // Tokens in chunks of PYR_CHUNK with every load of a chunk issued before the
+  // first is used, so a wave keeps PYR_CHUNK rows per tensor in flight instead
+  // of one; tokens are still summed in order.
+  int t = t0;
+  for (; t + PYR_CHUNK <= t1; t += PYR_CHUNK) {
+    uint4 cq[PYR_CHUNK], ck[PYR_CHUNK], cv[PYR_CHUNK];
+    float gq[PYR_CHUNK], gk[PYR_CHUNK];
+#pragma unroll
+    for (int i = 0; i < PYR_CHUNK; ++i) {
+      const int64_t o = xoff + (int64_t)(t + i) * a.ss;
+      cq[i] = ld16(a.xq + o);
+      ck[i] = ld16(a.xk + o);
+      cv[i] = ld16(a.xv + o);
+      gq[i] = GIVEN ? a.sqk[srow + t + i] : 0.f;
+      gk[i] = GIVEN ? a.skq[srow + t + i] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < PYR_CHUNK; ++i) token(t + i, cq[i], ck[i], cv[i], gq[i], gk[i]);
+  }
+  for (; t < t1; ++t) {
+    const int64_t o = xoff + (int64_t)t * a.ss;
+    token(t, ld16(a.xq + o), ld16(a.xk + o), ld16(a.xv + o), GIVEN ? a.sqk[srow + t] : 0.f,
+          GIVEN ? a.skq[srow + t] : 0.f);
   }
 }
 
@@ -249,7 +294,7 @@ int pyramid_fwd_impl(const void* xq, const void* xk, const void* xv, int64_t sb,
   const long long units = (long long)B * a.nspan * H;
   if (units > (1LL << 30)) return LH_ERR_UNSUPPORTED;
   a.units = (int)units;
-  for (int l = 1; l <= L; ++l) a.off[l] = g.off[l];
+  for (int l = 1; l <= L; ++l) { a.off[l] = g.off[l]; a.len[l] = g.len[l]; }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   switch (L - 1) {
     case 0: return launch_fwd<0>(a, given, st);

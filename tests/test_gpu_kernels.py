@@ -22,7 +22,8 @@ def _bf16_inputs(shape, n, seed, dev):
     return cpu, [c.to(dev) for c in cpu]
 
 
-@pytest.mark.parametrize("S,L,p,H", [(4096, 3, 4, 2), (4100, 3, 4, 2), (2048, 5, 2, 3), (1024, 2, 8, 1)])
+@pytest.mark.parametrize("S,L,p,H", [(4096, 3, 4, 2), (4100, 3, 4, 2), (2048, 5, 2, 3), (1024, 2, 8, 1),
+                                     (4096, 3, 32, 1), (2000, 6, 2, 1)])
 def test_pyramid_fwd(pkg, dev, S, L, p, H):
     print(f"pyramid S={S} L={L} p={p} H={H}", flush=True)
     cpu, gpu = _bf16_inputs((2, S, H, 128), 3, S + L, dev)
