@@ -626,8 +626,13 @@ __device__ __forceinline__ void store_qd(bf16_t* qt, bf16_t* dt, float* lt, cons
     *reinterpret_cast<u32x4*>(qt + (8 * w + 4 * i) * LH_D + 8 * lane) = x.q[i];
     *reinterpret_cast<u32x4*>(dt + (8 * w + 4 * i) * LH_D + 8 * lane) = x.d[i];
   }
-  if (w == 0) lt[lane] = x.ld;
-  if (w == 4) lt[BN + lane] = x.ld;
+  if (w == 0 || w == 4) {
+    // the lane index is recomputed here rather than kept live across the phase:
+    // at this point every VGPR is taken, and a kept address would be spilled
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    lt[(w == 0 ? 0 : BN) + l] = x.ld;
+  }
 }
 
 // this lane's gathered row indices (rows 8w + 4i + lane/16) of a tile, clamped
