@@ -42,6 +42,9 @@ constexpr int BMK = 128;  // keys per workgroup of the key-stationary kernel: 4 
 constexpr int QW = 8;     // waves per workgroup of the query-stationary kernels (32 queries each)
 constexpr int BN = 64;   // rows per LDS tile
 constexpr float RESCALE_LOG2 = 8.0f;
+constexpr int FWD_AHEAD = 8;  // forward: LDS operands read this many MFMAs ahead
+constexpr int DQ_AHEAD = 8;   // dQ kernel, S and dP products
+constexpr int DQ_AHEAD2 = 4;  // dQ kernel, dS K product
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -279,6 +282,9 @@ __device__ __forceinline__ void store_rows_bf16(bf16_t* row, const floatx16 (&ac
   }
 }
 
+#define SCHED_GROUP(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+constexpr int SG_MFMA = 0x008, SG_DSR = 0x100;
+
 // ===========================================================================
 // forward (query-stationary)
 // ===========================================================================
@@ -290,14 +296,27 @@ struct FwdState {
 
 __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], const bf16_t* Ks, const bf16_t* Vs,
                                          int k0, int my_q, int n, int lane, float sl2, bool mask) {
-  const int l32 = lane & 31, hh = lane >> 5;
+  const int hh = lane >> 5;
+  const LaneLds ll = lane_lds(lane);
   floatx16 s[2];
   __builtin_amdgcn_s_setprio(1);
+  {
+    // operand i: key block i & 1, k-slice i >> 1, so consecutive MFMAs feed
+    // different accumulators; each operand is read FWD_AHEAD MFMAs early
+    u32x4 kf[16];
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-    s[kb] = mfma(op_row(Ks, kb * 32 + l32, 0, hh), qf[0], floatx16{});
+    for (int i = 0; i < 16; ++i) kf[i] = lds_row(Ks, ll, i & 1, i >> 1);
+    s[0] = mfma(kf[0], qf[0], floatx16{});
+    s[1] = mfma(kf[1], qf[0], floatx16{});
 #pragma unroll
-    for (int c = 1; c < 8; ++c) s[kb] = mfma(op_row(Ks, kb * 32 + l32, c, hh), qf[c], s[kb]);
+    for (int i = 2; i < 16; ++i) s[i & 1] = mfma(kf[i], qf[i >> 1], s[i & 1]);
+    SCHED_GROUP(SG_DSR, FWD_AHEAD);
+#pragma unroll
+    for (int i = 0; i < 16 - FWD_AHEAD; ++i) {
+      SCHED_GROUP(SG_DSR, 1);
+      SCHED_GROUP(SG_MFMA, 1);
+    }
+    SCHED_GROUP(SG_MFMA, FWD_AHEAD);
   }
   __builtin_amdgcn_s_setprio(0);
   if (mask) {  // wave-uniform: only tiles that cross the diagonal or the end
@@ -345,13 +364,22 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
     pf[kb][1] = pack_frag(s[kb], 1);
   }
   __builtin_amdgcn_s_setprio(1);
+  {
+    // operand i: column block i & 3 (consecutive MFMAs feed different
+    // accumulators), key rows 32 (i >> 3) + 16 ((i >> 2) & 1); two transposing
+    // reads each, FWD_AHEAD operands ahead of their MFMAs
+    u32x4 vf[16];
 #pragma unroll
-  for (int d = 0; d < 4; ++d) {
+    for (int i = 0; i < 16; ++i) vf[i] = lds_tr(Vs, ll, (i >> 3) * 32 + 16 * ((i >> 2) & 1), i & 3);
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int i = 0; i < 16; ++i) st.o[i & 3] = mfma(vf[i], pf[i >> 3][(i >> 2) & 1], st.o[i & 3]);
+    SCHED_GROUP(SG_DSR, 2 * FWD_AHEAD);
 #pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) st.o[d] = mfma(op_tr(Vs, kb * 32 + 16 * c2, d, lane), pf[kb][c2], st.o[d]);
+    for (int i = 0; i < 16 - FWD_AHEAD; ++i) {
+      SCHED_GROUP(SG_DSR, 2);
+      SCHED_GROUP(SG_MFMA, 1);
     }
+    SCHED_GROUP(SG_MFMA, FWD_AHEAD);
   }
   __builtin_amdgcn_s_setprio(0);
 }
@@ -445,16 +473,32 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArg
 __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], const u32x4 (&qf)[8], const u32x4 (&df)[8],
                                         const bf16_t* Ks, const bf16_t* Vs, int k0, int my_q, int n, int lane,
                                         float sl2, float nlse, float dlt, bool mask) {
-  const int l32 = lane & 31, hh = lane >> 5;
+  const int hh = lane >> 5;
+  const LaneLds ll = lane_lds(lane);
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
+    floatx16 s, dp;
     __builtin_amdgcn_s_setprio(1);
-    floatx16 s = mfma(op_row(Ks, kb * 32 + l32, 0, hh), qf[0], floatx16{});
-    floatx16 dp = mfma(op_row(Vs, kb * 32 + l32, 0, hh), df[0], floatx16{});
+    {
+      // operand i: k-slice i >> 1 of K (i even, for S) or V (i odd, for dP), so
+      // consecutive MFMAs feed the two accumulators; reads run DQ_AHEAD ahead
+      u32x4 f[16];
 #pragma unroll
-    for (int c = 1; c < 8; ++c) {
-      s = mfma(op_row(Ks, kb * 32 + l32, c, hh), qf[c], s);
-      dp = mfma(op_row(Vs, kb * 32 + l32, c, hh), df[c], dp);
+      for (int i = 0; i < 16; ++i) f[i] = lds_row((i & 1) ? Vs : Ks, ll, kb, i >> 1);
+      s = mfma(f[0], qf[0], floatx16{});
+      dp = mfma(f[1], df[0], floatx16{});
+#pragma unroll
+      for (int i = 2; i < 16; i += 2) {
+        s = mfma(f[i], qf[i >> 1], s);
+        dp = mfma(f[i + 1], df[i >> 1], dp);
+      }
+      SCHED_GROUP(SG_DSR, DQ_AHEAD);
+#pragma unroll
+      for (int i = 0; i < 16 - DQ_AHEAD; ++i) {
+        SCHED_GROUP(SG_DSR, 1);
+        SCHED_GROUP(SG_MFMA, 1);
+      }
+      SCHED_GROUP(SG_MFMA, DQ_AHEAD);
     }
     __builtin_amdgcn_s_setprio(0);
     if (mask) {
@@ -468,10 +512,20 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], const u32x4 (&qf)[8]
     for (int v = 0; v < 16; ++v) s[v] = ex2(fmaf(s[v], sl2, nlse)) * (dp[v] - dlt);
     const u32x4 f0 = pack_frag(s, 0), f1 = pack_frag(s, 1);
     __builtin_amdgcn_s_setprio(1);
+    {
+      // operand i: column block i & 3, key rows kb * 32 + 16 (i >> 2)
+      u32x4 g[8];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      acc[d] = mfma(op_tr(Ks, kb * 32, d, lane), f0, acc[d]);
-      acc[d] = mfma(op_tr(Ks, kb * 32 + 16, d, lane), f1, acc[d]);
+      for (int i = 0; i < 8; ++i) g[i] = lds_tr(Ks, ll, kb * 32 + 16 * (i >> 2), i & 3);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i & 3] = mfma(g[i], (i >> 2) ? f1 : f0, acc[i & 3]);
+      SCHED_GROUP(SG_DSR, 2 * DQ_AHEAD2);
+#pragma unroll
+      for (int i = 0; i < 8 - DQ_AHEAD2; ++i) {
+        SCHED_GROUP(SG_DSR, 2);
+        SCHED_GROUP(SG_MFMA, 1);
+      }
+      SCHED_GROUP(SG_MFMA, DQ_AHEAD2);
     }
     __builtin_amdgcn_s_setprio(0);
   }
@@ -641,8 +695,6 @@ __device__ __forceinline__ void load_rows8(int (&r)[2], const BhRows& m, int row
   for (int i = 0; i < 2; ++i) r[i] = m.idx[min(row0 + 8 * w + 4 * i + (lane >> 4), m.last)];
 }
 
-#define SCHED_GROUP(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
-constexpr int SG_MFMA = 0x008, SG_DSR = 0x100;
 
 // Issue order of an MFMA phase built as: 16 transposing reads (8 operands),
 // 16 more, their 8 + 8 MFMAs, 8 + 8 row reads, their 8 + 8 MFMAs.  Each
