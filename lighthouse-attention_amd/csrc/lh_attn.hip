@@ -151,8 +151,28 @@ __device__ __forceinline__ u32x2 ld_tr16(const bf16_t* p) {
   return __builtin_bit_cast(u32x2, v);
 }
 
+// LDS byte address of a __shared__ pointer (wave-uniform)
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)(p));
+}
+
+// Direct global->LDS loads: lane l writes its 16 (g2l16) or 4 (g2l4) bytes at
+// lds_base + 16 l (4 l); lds_base is wave-uniform and goes through M0.  They
+// are issued as inline assembly: the compiler's wait-count bookkeeping treats
+// the builtin as a FLAT access that may also touch LDS and then turns every
+// later LDS-read wait of the wave into lgkmcnt(0), which serialises the
+// operand reads that feed the MFMAs.  Their completion is tracked by the
+// vector-memory counter only; every caller waits for it explicitly (wait_vm,
+// wait_loads) before a barrier publishes the data.  Loads the compiler does
+// know about stay correctly waited: the counter completes in order, so an
+// extra untracked load only makes the compiler's counts conservative.
 __device__ __forceinline__ void g2l16(const bf16_t* g, bf16_t* lds_base) {
-  __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_base, 16, 0, 0);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr(lds_base))
+               : "memory", "m0");
+}
+__device__ __forceinline__ void g2l4(const void* g, void* lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_addr(lds_base))
+               : "memory", "m0");
 }
 
 // wait until at most N vector-memory operations of this wave are outstanding
@@ -604,104 +624,63 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const Attn
 // one; in its VALU phase dS = P (dP - delta).  The dS waves run one phase
 // behind, and a block barrier closes every phase, so on each SIMD one wave
 // feeds the matrix core while the other runs its VALU work, and each wave needs
-// only half of the key-side registers.  Q/dO tiles (+ -lse, delta) rotate
-// through 4 LDS buffers; tile t is read in phases 2t .. 2t+3, and every wave
-// copies its 8 rows of tile j+2 into LDS in the VALU phase of step j (loaded
-// into registers one step earlier).  Deterministic: no atomics.
+// only half of the key-side registers.  The S and dP accumulators start from
+// -lse / (scale log2 e) and delta of their query (the dS waves hold -V, so
+// their accumulator ends as delta - dP): the VALU phases read nothing from LDS
+// but the exchanged P, because reads issued there would queue behind the
+// partner waves' operand reads.  Q/dO tiles (+ lse, delta) rotate through 4
+// LDS buffers, filled by direct loads that the VALU phases issue (the P waves
+// the Q tiles, the dS waves the dO tiles).  Deterministic: no atomics.
 // ===========================================================================
 __device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// Row indices (through the selected-index map when GATHER) of the rows this
-// lane copies in a 64-row tile at row0 (wave w: rows 8w + 4i + lane/16,
-// i = 0, 1), clamped to the last row.  Gathered indices are 8 consecutive
-// entries read at a wave-uniform address with scalar loads (needs n >= 8).
-template <bool GATHER>
-__device__ __forceinline__ void tile_rows(int (&r)[2], const BhRows& m, int row0, int w, int lane) {
-  const int g = lane >> 4;
-  if (!GATHER) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) r[i] = min(row0 + 8 * w + 4 * i + g, m.last);
-    return;
-  }
-  const int first = __builtin_amdgcn_readfirstlane(row0 + 8 * w);
-  const int base = min(first, m.last - 7);
-  // the index map is read-only here: reading it through the constant address
-  // space lets the loads be scalar
-  typedef const __attribute__((address_space(4))) int cint;
-  cint* p = (cint*)(m.idx + base);
-  int v[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) v[k] = p[k];
-  if (first + 7 <= m.last) {  // no clamping: row 4i + g is entry 4i + g
-#pragma unroll
-    for (int i = 0; i < 2; ++i) r[i] = g == 0 ? v[4 * i] : g == 1 ? v[4 * i + 1] : g == 2 ? v[4 * i + 2] : v[4 * i + 3];
-  } else {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int k = min(first + 4 * i + g, m.last) - base;
-      int x = v[0];
-#pragma unroll
-      for (int kk = 1; kk < 8; ++kk) x = k == kk ? v[kk] : x;
-      r[i] = x;
-    }
-  }
-}
-
-// This wave's 8 rows of a Q tile (gathered) and dO tile (dense), plus the
-// tile's lse (wave 0) or delta (wave 4), staged in registers: loaded at the
-// start of a VALU phase and written to LDS at its end, so the loads' latency
-// is covered by the phase's VALU work and no load is in flight across a
-// barrier.
-struct QdRegs {
-  u32x4 q[2], d[2];
-  float ld;
-};
-
-__device__ __forceinline__ void load_qd(QdRegs& x, const BhRows& m, const int (&r)[2], const AttnArgs& a,
-                                        int64_t bhn, int row0, int n, int w, int lane) {
+// Tile copies of the key-stationary kernel: direct global->LDS loads, each wave
+// 16 rows of a 64-row tile (four 1 KB loads, row 16 w + 4 i + lane / 16 in
+// load i), plus at most one 64-entry row of 4-byte values.
+__device__ __forceinline__ void copy_q16(bf16_t* qt, const BhRows& m, const int (&r)[4], int w, int lane) {
   const int rsub = lane >> 4, slot = lane & 15;
-  const bf16_t* dbase = a.dout + bhn * LH_D;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int row = 8 * w + 4 * i + rsub;
-    const int chunk = 8 * (slot ^ swz(row));
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * w + 4 * i + rsub;
     const bool pooled = r[i] >= m.split;
     const uint32_t rel = (uint32_t)(r[i] - (pooled ? m.split : 0));
-    x.q[i] = ldg16((pooled ? m.qp : m.q) + rel * (uint32_t)(pooled ? m.ps : m.ss) + chunk);
-    x.d[i] = ldg16(dbase + (uint32_t)min(row0 + row, n - 1) * LH_D + chunk);
+    g2l16((pooled ? m.qp : m.q) + rel * (uint32_t)(pooled ? m.ps : m.ss) + 8 * (slot ^ swz(row)),
+          qt + (16 * w + 4 * i) * LH_D);
   }
-  if (w == 0) x.ld = a.lse_in[bhn + min(row0 + lane, n - 1)];
-  if (w == 4) x.ld = a.delta[bhn + min(row0 + lane, n - 1)];
 }
 
-__device__ __forceinline__ void store_qd(bf16_t* qt, bf16_t* dt, float* lt, const QdRegs& x, int w, int lane) {
+__device__ __forceinline__ void copy_d16(bf16_t* dt, const bf16_t* dbase, int row0, int n, int w, int lane) {
+  const int rsub = lane >> 4, slot = lane & 15;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    *reinterpret_cast<u32x4*>(qt + (8 * w + 4 * i) * LH_D + 8 * lane) = x.q[i];
-    *reinterpret_cast<u32x4*>(dt + (8 * w + 4 * i) * LH_D + 8 * lane) = x.d[i];
-  }
-  if (w == 0 || w == 4) {
-    // the lane index is recomputed here rather than kept live across the phase:
-    // at this point every VGPR is taken, and a kept address would be spilled
-    int l;
-    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
-    lt[(w == 0 ? 0 : BN) + l] = x.ld;
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * w + 4 * i + rsub;
+    g2l16(dbase + (uint32_t)min(row0 + row, n - 1) * LH_D + 8 * (slot ^ swz(row)), dt + (16 * w + 4 * i) * LH_D);
   }
 }
 
-// this lane's gathered row indices (rows 8w + 4i + lane/16) of a tile, clamped
-__device__ __forceinline__ void load_rows8(int (&r)[2], const BhRows& m, int row0, int w, int lane) {
+// Selected-row indices of the rows wave w copies in a 64-row tile at row0
+// (clamped to the last row), read from global memory.
+template <bool GATHER>
+__device__ __forceinline__ void rows16(int (&r)[4], const BhRows& m, int row0, int w, int lane) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i) r[i] = m.idx[min(row0 + 8 * w + 4 * i + (lane >> 4), m.last)];
+  for (int i = 0; i < 4; ++i) {
+    const int s = min(row0 + 16 * w + 4 * i + (lane >> 4), m.last);
+    r[i] = GATHER ? m.idx[s] : s;
+  }
 }
 
+// The same indices from a tile's 64 entries staged in LDS.
+__device__ __forceinline__ void rows16_lds(int (&r)[4], const int* ix, int w, int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = ix[16 * w + 4 * i + (lane >> 4)];
+}
 
 // Issue order of an MFMA phase built as: 16 transposing reads (8 operands),
 // 16 more, their 8 + 8 MFMAs, 8 + 8 row reads, their 8 + 8 MFMAs.  Each
 // operand group is read while the previous group's MFMAs run, so LDS latency
 // overlaps the matrix core and at most two operand groups are live.
 __device__ __forceinline__ void mma_phase_order() {
-  SCHED_GROUP(SG_DSR, 16);
+  SCHED_GROUP(SG_DSR, 24);  // the 8 accumulator-init reads, then the first 8 operands
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     SCHED_GROUP(SG_DSR, 2);
@@ -724,7 +703,22 @@ __device__ __forceinline__ void mma_phase_order() {
 // S of the current tile (Qc).  Operands are read a group ahead of their MFMAs.
 __device__ __forceinline__ void pw_mma(floatx16 (&s)[2], floatx16 (&dva)[4], const u32x4 (&kf)[8],
                                        const u32x4 (&pp)[2][2], const bf16_t* Qc, const bf16_t* Dp,
-                                       const LaneLds& ll) {
+                                       const LaneLds& ll, const float* lse, float nisl2) {
+  // S starts from -lse / (scale log2 e) of its query, so that P = exp2(S scale log2 e)
+  floatx16 si[2];
+  {
+    const int hh = __lane_id() >> 5;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 l4 = *reinterpret_cast<const float4*>(lse + qb * 32 + 8 * g + 4 * hh);
+        si[qb][4 * g + 0] = l4.x * nisl2;
+        si[qb][4 * g + 1] = l4.y * nisl2;
+        si[qb][4 * g + 2] = l4.z * nisl2;
+        si[qb][4 * g + 3] = l4.w * nisl2;
+      }
+  }
   u32x4 oa[8], ob[8], ka[8], kb[8];
   // operand i: rows 32 qb + 16 c2 with qb = i & 1, c2 = (i >> 1) & 1; column block db = i >> 2 (+2)
 #pragma unroll
@@ -739,10 +733,10 @@ __device__ __forceinline__ void pw_mma(floatx16 (&s)[2], floatx16 (&dva)[4], con
   for (int i = 0; i < 8; ++i) dva[2 + (i >> 2)] = mfma(ob[i], pp[i & 1][(i >> 1) & 1], dva[2 + (i >> 2)]);
 #pragma unroll
   for (int c = 0; c < 8; ++c) kb[c] = lds_row(Qc, ll, 1, c);
-  s[0] = mfma(ka[0], kf[0], floatx16{});
+  s[0] = mfma(ka[0], kf[0], si[0]);
 #pragma unroll
   for (int c = 1; c < 8; ++c) s[0] = mfma(ka[c], kf[c], s[0]);
-  s[1] = mfma(kb[0], kf[0], floatx16{});
+  s[1] = mfma(kb[0], kf[0], si[1]);
 #pragma unroll
   for (int c = 1; c < 8; ++c) s[1] = mfma(kb[c], kf[c], s[1]);
 
@@ -753,7 +747,22 @@ __device__ __forceinline__ void pw_mma(floatx16 (&s)[2], floatx16 (&dva)[4], con
 // dP of the current tile (Dc).
 __device__ __forceinline__ void dw_mma(floatx16 (&dp)[2], floatx16 (&dka)[4], const u32x4 (&vf)[8],
                                        const u32x4 (&dsf)[2][2], const bf16_t* Dc, const bf16_t* Qp,
-                                       const LaneLds& ll) {
+                                       const LaneLds& ll, const float* delta) {
+  // vf holds -V, and the accumulator starts from delta of its query: it ends as delta - dP
+  floatx16 di[2];
+  {
+    const int hh = __lane_id() >> 5;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 d4 = *reinterpret_cast<const float4*>(delta + qb * 32 + 8 * g + 4 * hh);
+        di[qb][4 * g + 0] = d4.x;
+        di[qb][4 * g + 1] = d4.y;
+        di[qb][4 * g + 2] = d4.z;
+        di[qb][4 * g + 3] = d4.w;
+      }
+  }
   u32x4 oa[8], ob[8], ka[8], kb[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) oa[i] = lds_tr(Qp, ll, 32 * (i & 1) + 16 * ((i >> 1) & 1), i >> 2);
@@ -767,10 +776,10 @@ __device__ __forceinline__ void dw_mma(floatx16 (&dp)[2], floatx16 (&dka)[4], co
   for (int i = 0; i < 8; ++i) dka[2 + (i >> 2)] = mfma(ob[i], dsf[i & 1][(i >> 1) & 1], dka[2 + (i >> 2)]);
 #pragma unroll
   for (int c = 0; c < 8; ++c) kb[c] = lds_row(Dc, ll, 1, c);
-  dp[0] = mfma(ka[0], vf[0], floatx16{});
+  dp[0] = mfma(ka[0], vf[0], di[0]);
 #pragma unroll
   for (int c = 1; c < 8; ++c) dp[0] = mfma(ka[c], vf[c], dp[0]);
-  dp[1] = mfma(kb[0], vf[0], floatx16{});
+  dp[1] = mfma(kb[0], vf[0], di[1]);
 #pragma unroll
   for (int c = 1; c < 8; ++c) dp[1] = mfma(kb[c], vf[c], dp[1]);
 
@@ -783,6 +792,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
   __shared__ __attribute__((aligned(1024))) bf16_t D0[TILE], D1[TILE], D2[TILE], D3[TILE];
   __shared__ __attribute__((aligned(16))) float L0[2 * BN], L1[2 * BN], L2[2 * BN], L3[2 * BN];  // lse, delta
   __shared__ u32x4 EX[4][4][64];  // P handed from each P wave to its dS wave
+  __shared__ __attribute__((aligned(16))) int IX[4][BN];  // selected-row indices of the Q tiles to copy
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = wave >> 2, pair = wave & 3;
@@ -793,40 +803,57 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
   const BhRows m = bh_rows(a, bh);
   const int k0 = kblk * BMK, kw = k0 + 32 * pair, my_k = kw + l32;
 
-  u32x4 kf[8];  // K (P wave) or V (dS wave) rows of this lane's key
+  u32x4 kf[8];  // K (P wave) or -V (dS wave) rows of this lane's key
   {
     bool pooled;
     const uint32_t o = row_off(m, my_k, pooled) + 8 * hh;
     const bf16_t* p = grp ? (pooled ? m.vp : m.v) + o : (pooled ? m.kp : m.k) + o;
 #pragma unroll
     for (int c = 0; c < 8; ++c) kf[c] = ldg16(p + 16 * c);
+    if (grp) {  // the dS waves hold -V (bf16 sign flips are exact)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) kf[c] ^= 0x80008000u;
+    }
   }
   const int64_t bhn = (int64_t)bh * n;
+  const bf16_t* dbase = a.dout + bhn * LH_D;
+  const float* lse_row = a.lse_in + bhn;
+  const float* dlt_row = a.delta + bhn;
   const int jt0 = k0 / BN;  // first query tile that sees these keys
   const int nt = (n + BN - 1) / BN;
 
-  // Each wave copies rows 8w .. 8w+7 of every tile (the P waves the first
-  // half, the dS waves the second).  In step j the P waves copy tile j+2 and
-  // the dS waves tile j+3 (lead); tiles jt0, jt0+1 (and the dS waves' half of
-  // jt0+2) are copied here.
-  const int lead = grp ? 3 : 2;
-  int rr[2];  // row indices of the next tile this wave copies
-  {
-    QdRegs x;
-    for (int t = jt0; t < jt0 + lead; ++t) {
-      if (GATHER)
-        load_rows8(rr, m, t * BN, wave, lane);
-      else
-        tile_rows<false>(rr, m, t * BN, wave, lane);
-      load_qd(x, m, rr, a, bhn, t * BN, n, wave, lane);
-      const int b = t - jt0;
-      store_qd(b == 0 ? Q0 : b == 1 ? Q1 : Q2, b == 0 ? D0 : b == 1 ? D1 : D2, b == 0 ? L0 : b == 1 ? L1 : L2, x,
-               wave, lane);
+  // Copies.  The P waves copy the Q tiles (+ lse on wave 0, the Q row indices
+  // of a later tile on wave 1), the dS waves the dO tiles (+ delta on wave 4),
+  // each wave 16 rows, in their VALU phases: in step j the P waves copy tile
+  // j + 2 (phase 2j + 1) and the dS waves tile j + 3 (phase 2j + 2), each into
+  // the buffer last read in phase 2j - 1 (Q, lse) or 2j (dO, delta); every
+  // wave waits for its previous step's copies before the barrier closing its
+  // VALU phase, so tile t is in LDS from phase 2t on (Q) or 2t + 1 on (dO).
+  // Here: Q tiles jt0, jt0 + 1, dO tiles jt0 .. jt0 + 2, and the indices of
+  // Q tiles jt0 + 2, jt0 + 3.
+  if (grp == 0) {
+    int r[4];
+    rows16<GATHER>(r, m, jt0 * BN, pair, lane);
+    copy_q16(Q0, m, r, pair, lane);
+    rows16<GATHER>(r, m, (jt0 + 1) * BN, pair, lane);
+    copy_q16(Q1, m, r, pair, lane);
+    if (pair == 0) {
+      g2l4(lse_row + min(jt0 * BN + lane, n - 1), L0);
+      g2l4(lse_row + min((jt0 + 1) * BN + lane, n - 1), L1);
     }
-    if (GATHER)
-      load_rows8(rr, m, (jt0 + lead) * BN, wave, lane);
-    else
-      tile_rows<false>(rr, m, (jt0 + lead) * BN, wave, lane);
+    if (GATHER && pair == 1) {
+      g2l4(m.idx + min((jt0 + 2) * BN + lane, m.last), IX[2]);
+      g2l4(m.idx + min((jt0 + 3) * BN + lane, m.last), IX[3]);
+    }
+  } else {
+    copy_d16(D0, dbase, jt0 * BN, n, pair, lane);
+    copy_d16(D1, dbase, (jt0 + 1) * BN, n, pair, lane);
+    copy_d16(D2, dbase, (jt0 + 2) * BN, n, pair, lane);
+    if (pair == 0) {
+      g2l4(dlt_row + min(jt0 * BN + lane, n - 1), L0 + BN);
+      g2l4(dlt_row + min((jt0 + 1) * BN + lane, n - 1), L1 + BN);
+      g2l4(dlt_row + min((jt0 + 2) * BN + lane, n - 1), L2 + BN);
+    }
   }
   // the first step's dV / dK terms multiply zeros with buffer 3: make it finite
 #pragma unroll
@@ -834,39 +861,37 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
     reinterpret_cast<u32x4*>(Q3)[tid + 512 * i] = u32x4{};
     reinterpret_cast<u32x4*>(D3)[tid + 512 * i] = u32x4{};
   }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the first tiles and the zeros are in LDS
+  wait_loads();  // the first tiles and the zeros are in LDS
   block_barrier();
 
   floatx16 acc[4];  // dV (P wave) or dK (dS wave)
 #pragma unroll
   for (int d = 0; d < 4; ++d) acc[d] = floatx16{};
-  floatx16 sc[2] = {floatx16{}, floatx16{}};  // S (P wave) or dP (dS wave)
+  floatx16 sc[2] = {floatx16{}, floatx16{}};  // S - lse/(scale log2 e) (P wave) or delta - dP (dS wave)
   u32x4 op[2][2] = {{u32x4{}, u32x4{}}, {u32x4{}, u32x4{}}};  // P or dS, bf16 operands
-  const float sl2 = a.sl2;
+  const float sl2 = a.sl2, nisl2 = -1.0f / a.sl2;
 
-  // Step j: MFMA phase (tile j, and the previous tile's accumulation), then
-  // VALU phase, which also copies tile j + lead into the buffer of tile
-  // j + lead - 4 (last read in phase 2j-1 by a P wave's copy, 2j+1 by a dS
-  // wave's); the copies land before the phase's closing barrier.  The step
-  // count is rounded up to a multiple of 4 so that the buffers rotate
-  // statically; steps past the last tile copy clamped rows.  Each role runs its
-  // own loop (same barrier count) and is register-allocated on its own.
-  QdRegs xs;
-  auto copy_begin = [&](int j) {
-    const int t = j + lead;
-    load_qd(xs, m, rr, a, bhn, t * BN, n, wave, lane);
-    if (GATHER)
-      load_rows8(rr, m, (t + 1) * BN, wave, lane);
-    else
-      tile_rows<false>(rr, m, (t + 1) * BN, wave, lane);
-  };
-  auto copy_end = [&](bf16_t* Qn, bf16_t* Dn, float* Ln) { store_qd(Qn, Dn, Ln, xs, wave, lane); };
-  auto pstep = [&](int j, const bf16_t* Qc, const float* Lc, const bf16_t* Dp, bf16_t* Qn, bf16_t* Dn, float* Ln) {
+  // Step j: MFMA phase (tile j, and the previous tile's accumulation), then the
+  // VALU phase with this step's copies.  The step count is rounded up to a
+  // multiple of 4 so that the buffers rotate statically; steps past the last
+  // tile copy clamped rows.  Each role runs its own loop (same barrier count)
+  // and is register-allocated on its own.
+  auto pstep = [&](int j, const bf16_t* Qc, const float* Lc, const bf16_t* Dp, bf16_t* Qn, float* Ln,
+                   const int* ixc, int* ixn) {
     __builtin_amdgcn_s_setprio(1);
-    pw_mma(sc, acc, kf, op, Qc, Dp, ll);
+    pw_mma(sc, acc, kf, op, Qc, Dp, ll, Lc, nisl2);
     __builtin_amdgcn_s_setprio(0);
     block_barrier();
-    copy_begin(j);
+    {  // copy Q tile j + 2 (indices staged two steps ago), its lse, and the indices of tile j + 4
+      int r[4];
+      if (GATHER)
+        rows16_lds(r, ixc, pair, lane);
+      else
+        rows16<false>(r, m, (j + 2) * BN, pair, lane);
+      copy_q16(Qn, m, r, pair, lane);
+      if (pair == 0) g2l4(lse_row + min((j + 2) * BN + lane, n - 1), Ln);
+      if (GATHER && pair == 1) g2l4(m.idx + min((j + 4) * BN + lane, m.last), ixn);
+    }
     if (j < nt) {  // P = exp2(S sl2 - lse), masked causally and past n
       const int q0t = j * BN;
       const bool mask = q0t < kw + 31 || q0t + BN > n;
@@ -880,12 +905,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
           }
         }
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const float4 l4 = *reinterpret_cast<const float4*>(Lc + qb * 32 + 8 * g + 4 * hh);  // lse
-          const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) sc[qb][4 * g + e] = ex2(fmaf(sc[qb][4 * g + e], sl2, -lv[e]));
-        }
+        for (int v = 0; v < 16; ++v) sc[qb][v] = ex2(sc[qb][v] * sl2);
         op[qb][0] = pack_frag(sc[qb], 0);
         op[qb][1] = pack_frag(sc[qb], 1);
       }
@@ -894,16 +914,21 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
     } else {  // past the last tile the accumulation steps add zeros
       op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
     }
-    copy_end(Qn, Dn, Ln);
+    // all but this step's copies have landed
+    if (pair == 0 || (GATHER && pair == 1))
+      wait_vm<5>();
+    else
+      wait_vm<4>();
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this phase's LDS writes have landed
     block_barrier();
   };
-  auto dstep = [&](int j, const bf16_t* Dc, const float* Lc, const bf16_t* Qp, bf16_t* Qn, bf16_t* Dn, float* Ln) {
+  auto dstep = [&](int j, const bf16_t* Dc, const float* Lc, const bf16_t* Qp, bf16_t* Dn, float* Ln) {
     __builtin_amdgcn_s_setprio(1);
-    dw_mma(sc, acc, kf, op, Dc, Qp, ll);
+    dw_mma(sc, acc, kf, op, Dc, Qp, ll, Lc + BN);
     __builtin_amdgcn_s_setprio(0);
     block_barrier();
-    copy_begin(j);
+    copy_d16(Dn, dbase, (j + 3) * BN, n, pair, lane);  // dO tile j + 3 and its delta
+    if (pair == 0) g2l4(dlt_row + min((j + 3) * BN + lane, n - 1), Ln + BN);
     if (j < nt) {  // dS = P (dP - delta), P from the partner P wave
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
@@ -912,37 +937,35 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
         unpack8(uint4{e0.x, e0.y, e0.z, e0.w}, pv);
         unpack8(uint4{e1.x, e1.y, e1.z, e1.w}, pv + 8);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const float4 d4 = *reinterpret_cast<const float4*>(Lc + BN + qb * 32 + 8 * g + 4 * hh);  // delta
-          const float dd[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) sc[qb][4 * g + e] = pv[4 * g + e] * (sc[qb][4 * g + e] - dd[e]);
-        }
+        for (int v = 0; v < 16; ++v) sc[qb][v] = pv[v] * -sc[qb][v];  // P (dP - delta)
         op[qb][0] = pack_frag(sc[qb], 0);
         op[qb][1] = pack_frag(sc[qb], 1);
       }
     } else {
       op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
     }
-    copy_end(Qn, Dn, Ln);
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the copies have landed, the partner's P was read
+    if (pair == 0)
+      wait_vm<5>();
+    else
+      wait_vm<4>();
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the partner's P was read
     block_barrier();
   };
   if (grp == 0) {
     for (int j = jt0; j <= nt; j += 4) {
-      pstep(j, Q0, L0, D3, Q2, D2, L2);
-      pstep(j + 1, Q1, L1, D0, Q3, D3, L3);
-      pstep(j + 2, Q2, L2, D1, Q0, D0, L0);
-      pstep(j + 3, Q3, L3, D2, Q1, D1, L1);
+      pstep(j, Q0, L0, D3, Q2, L2, IX[2], IX[0]);
+      pstep(j + 1, Q1, L1, D0, Q3, L3, IX[3], IX[1]);
+      pstep(j + 2, Q2, L2, D1, Q0, L0, IX[0], IX[2]);
+      pstep(j + 3, Q3, L3, D2, Q1, L1, IX[1], IX[3]);
     }
     block_barrier();
   } else {
     block_barrier();  // the dS waves run one phase behind
     for (int j = jt0; j <= nt; j += 4) {
-      dstep(j, D0, L0, Q3, Q3, D3, L3);
-      dstep(j + 1, D1, L1, Q0, Q0, D0, L0);
-      dstep(j + 2, D2, L2, Q1, Q1, D1, L1);
-      dstep(j + 3, D3, L3, Q2, Q2, D2, L2);
+      dstep(j, D0, L0, Q3, D3, L3);
+      dstep(j + 1, D1, L1, Q0, D0, L0);
+      dstep(j + 2, D2, L2, Q1, D1, L1);
+      dstep(j + 3, D3, L3, Q2, D2, L2);
     }
   }
   if (my_k >= n) return;
