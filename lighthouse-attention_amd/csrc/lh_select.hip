@@ -1,9 +1,11 @@
 // Hierarchical per-tile top-k selection for gfx950.
 //
-// One 64-lane wave per (b, h, tile).  The 128-element working set of the
-// reference block (src/lighthouse_selection_cuda.py:150-157) lives in
-// registers: element e = 64*slot + lane.  Compare-exchanges at distance 64 are
-// in-lane; distances 1..32 are cross-lane shuffles.  The network, the batch
+// One 4-wave workgroup per (b, h, tile).  The 128-element working set of the
+// reference block (src/lighthouse_selection_cuda.py:150-157) lives in the
+// registers of one wave: element e = 64*slot + lane.  Compare-exchanges at
+// distance 64 are in-lane; distances 1..32 are cross-lane shuffles.  Wave 0
+// runs the qk sorts and wave 1 the kq sorts, one batch behind, the qk rejects
+// handed over in LDS; all four waves load candidates, rank and emit.  The network, the batch
 // structure and the candidate order follow src/lighthouse_selection_cuda.py:
 //   - sort network:                 :41-110 (strict compare-exchange)
 //   - candidates (coarsest/children): :177-229
@@ -41,14 +43,15 @@ struct SelParams {
 
 // ---------------------------------------------------------------------------
 // Value of lane ^ J without a round trip through LDS: DPP quad permutes for 1
-// and 2, a 16-lane row rotation by 8 for 8, the gfx950 row/half swaps for 16
-// and 32; only 4 uses ds_swizzle (no memory access).
+// and 2, a half-row mirror followed by a quad reversal for 4, a 16-lane row
+// rotation by 8 for 8, the gfx950 row/half swaps for 16 and 32.
 // ---------------------------------------------------------------------------
 template <int J>
 __device__ __forceinline__ int lane_xor(int v, int lane) {
   if constexpr (J == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);  // quad_perm [1,0,3,2]
   else if constexpr (J == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);  // quad_perm [2,3,0,1]
-  else if constexpr (J == 4) return __builtin_amdgcn_ds_swizzle(v, 0x101F);  // swap groups of 4 (xor mask 4)
+  else if constexpr (J == 4)  // row_half_mirror (i -> 7 - i in each 8 lanes), then quad_perm [3,2,1,0]
+    return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true), 0x1B, 0xF, 0xF, true);
   else if constexpr (J == 8) return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, true);  // row_ror:8
   else if constexpr (J == 16) {
     const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
@@ -123,20 +126,22 @@ __device__ __forceinline__ bool get_bit(const uint32_t* bits, int i) {
 }
 
 template <int TIE>
-__global__ __launch_bounds__(64) void select_kernel(const float* __restrict__ sqk,
-                                                    const float* __restrict__ skq,
-                                                    int32_t* __restrict__ indices,
-                                                    int32_t* __restrict__ inverse,
-                                                    const SelParams P) {
+__global__ __launch_bounds__(256) void select_kernel(const float* __restrict__ sqk,
+                                                     const float* __restrict__ skq,
+                                                     int32_t* __restrict__ indices,
+                                                     int32_t* __restrict__ inverse,
+                                                     const SelParams P) {
   const int tile = blockIdx.x;
   const int bh = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   extern __shared__ uint32_t smem[];
   float* sc_qk = reinterpret_cast<float*>(smem);
   float* sc_kq = sc_qk + P.nc_pad;
   int* cand = reinterpret_cast<int*>(sc_kq + P.nc_pad);
   int* parent = cand + P.nc_pad;
-  uint32_t* selbits = reinterpret_cast<uint32_t*>(parent + TOPK);
+  int* rej = parent + TOPK;  // [2][64]: qk rejects of a batch, handed from wave 0 to wave 1
+  uint32_t* selbits = reinterpret_cast<uint32_t*>(rej + 2 * HALF);
   uint32_t* kbits = selbits + P.sel_words;
   uint32_t* kpre = kbits + P.key_words;
 
@@ -144,18 +149,20 @@ __global__ __launch_bounds__(64) void select_kernel(const float* __restrict__ sq
   const float* k = skq + (size_t)bh * P.S_tot;
   const int L = P.L, p = P.p, shift = P.shift;
 
-  for (int w = lane; w < P.sel_words; w += 64) selbits[w] = 0u;
-  for (int w = lane; w < P.key_words; w += 64) kbits[w] = 0u;
-  parent[lane] = -1;
-  parent[lane + 64] = -1;
+  for (int w = tid; w < P.sel_words; w += 256) selbits[w] = 0u;
+  for (int w = tid; w < P.key_words; w += 256) kbits[w] = 0u;
+  if (tid < TOPK) parent[tid] = -1;
   __syncthreads();
 
   // ------------------------------------------------------------------ select
+  // Per level, batch b's qk sort (wave 0) and batch b-1's kq sort (wave 1)
+  // run side by side: the kq sort of a batch depends on its qk rejects and on
+  // the previous kq sort only, so the two streams are the reference's order.
   for (int level = L; level >= 2; --level) {
     const int off = P.off[level];
     const int nc = (level == L) ? P.NCC : p * TOPK;
     const int nb = (nc + HALF - 1) / HALF;
-    for (int a = lane; a < nb * HALF; a += 64) {
+    for (int a = tid; a < nb * HALF; a += 256) {
       int id = -1;
       if (a < nc) {
         if (level == L) {
@@ -172,32 +179,37 @@ __global__ __launch_bounds__(64) void select_kernel(const float* __restrict__ sq
     }
     __syncthreads();
 
-    float tq_s = SENT, tk_s = SENT;
-    int tq_x = -1, tk_x = -1, tq_i = -1, tk_i = -1;
-    for (int b = 0; b < nb; ++b) {
-      const int a = b * HALF + lane;
-      float s0 = tq_s, s1 = sc_qk[a];
-      int x0 = tq_x, x1 = cand[a] >= 0 ? a : -1;
-      int i0 = tq_i, i1 = TIE ? cand[a] : 0;
-      sort128<TIE>(s0, x0, i0, s1, x1, i1, lane);
-      tq_s = s0; tq_x = x0; tq_i = i0;
-      // qk rejects (positions 64..127) stream into the kq sort
-      const int r = x1;
-      float u0 = tk_s, u1 = r >= 0 ? sc_kq[r] : SENT;
-      int y0 = tk_x, y1 = r;
-      int j0 = tk_i, j1 = TIE ? i1 : 0;
-      sort128<TIE>(u0, y0, j0, u1, y1, j1, lane);
-      tk_s = u0; tk_x = y0; tk_i = j0;
+    float t_s = SENT;
+    int t_x = -1, t_i = -1;  // TQ (wave 0) or TK (wave 1)
+    for (int b = 0; b <= nb; ++b) {
+      if (wave == 0 && b < nb) {
+        const int a = b * HALF + lane;
+        float s0 = t_s, s1 = sc_qk[a];
+        int x0 = t_x, x1 = cand[a] >= 0 ? a : -1;
+        int i0 = t_i, i1 = TIE ? cand[a] : 0;
+        sort128<TIE>(s0, x0, i0, s1, x1, i1, lane);
+        t_s = s0; t_x = x0; t_i = i0;
+        rej[(b & 1) * HALF + lane] = x1;  // qk rejects (positions 64..127) stream into the kq sort
+      } else if (wave == 1 && b >= 1) {
+        const int r = rej[((b - 1) & 1) * HALF + lane];
+        float u0 = t_s, u1 = r >= 0 ? sc_kq[r] : SENT;
+        int y0 = t_x, y1 = r;
+        int j0 = t_i, j1 = TIE ? (r >= 0 ? cand[r] : -1) : 0;
+        sort128<TIE>(u0, y0, j0, u1, y1, j1, lane);
+        t_s = u0; t_x = y0; t_i = j0;
+      }
+      __syncthreads();
     }
-    const int idq = tq_x >= 0 ? cand[tq_x] : -1;
-    const int idk = tk_x >= 0 ? cand[tk_x] : -1;
+    const int id = (wave < 2 && t_x >= 0) ? cand[t_x] : -1;
     __syncthreads();  // every lane has read parent[] and cand[] for this level
-    parent[lane] = idq;
-    parent[lane + 64] = idk;
-    uint32_t* sb = selbits + P.selw_off[level];
-    const int base = tile * P.R[level];
-    if (idq >= 0) { const int t = idq - base; atomicOr(&sb[t >> 5], 1u << (t & 31)); }
-    if (idk >= 0) { const int t = idk - base; atomicOr(&sb[t >> 5], 1u << (t & 31)); }
+    if (wave < 2) {
+      parent[lane + HALF * wave] = id;  // [TQ | TK]
+      if (id >= 0) {
+        uint32_t* sb = selbits + P.selw_off[level];
+        const int t = id - tile * P.R[level];
+        atomicOr(&sb[t >> 5], 1u << (t & 31));
+      }
+    }
     __syncthreads();
   }
 
@@ -208,7 +220,7 @@ __global__ __launch_bounds__(64) void select_kernel(const float* __restrict__ sq
     const int Rl = P.R[level];
     const int base = tile * Rl;
     const int c_shift = (level - 1) * shift;  // log2 c_l
-    for (int j = lane; j < Rl; j += 64) {
+    for (int j = tid; j < Rl; j += 256) {
       const bool is_cand = (level == L) || get_bit(selbits + P.selw_off[level + 1], j >> shift);
       if (!is_cand) continue;
       const bool is_sel = (level >= 2) && get_bit(selbits + P.selw_off[level], j);
@@ -220,7 +232,7 @@ __global__ __launch_bounds__(64) void select_kernel(const float* __restrict__ sq
     }
   }
   __syncthreads();
-  {  // exclusive prefix of popcounts per key word
+  if (wave == 0) {  // exclusive prefix of popcounts per key word
     const int chunk = (P.key_words + 63) / 64;
     const int w0 = lane * chunk;
     const int w1 = min(w0 + chunk, P.key_words);
@@ -246,7 +258,7 @@ __global__ __launch_bounds__(64) void select_kernel(const float* __restrict__ sq
     const int c_shift = (level - 1) * shift;
     // the last tile also owns the trailing nodes that no tile visits
     const int jend = (inv && tile == P.T - 1) ? (P.len[level] - base) : Rl;
-    for (int j = lane; j < jend; j += 64) {
+    for (int j = tid; j < jend; j += 256) {
       int pos = -1;
       if (j < Rl) {
         const bool is_cand = (level == L) || get_bit(selbits + P.selw_off[level + 1], j >> shift);
@@ -346,16 +358,16 @@ extern "C" int lh_select_topk(const float* scores_qk, const float* scores_kq, in
   const long long span = (long long)P.NCC * ipow(p, L - 1) * (1LL << (L - 1));
   if ((long long)S * ipow(p, 0) * (1LL << (L - 1)) >= (1LL << 31)) return LH_ERR_UNSUPPORTED;
   P.key_words = (int)((span + 31) / 32);
-  const long long lds = 4LL * (3LL * P.nc_pad + TOPK + P.sel_words + 2LL * P.key_words);
+  const long long lds = 4LL * (3LL * P.nc_pad + TOPK + 2 * HALF + P.sel_words + 2LL * P.key_words);
   if (lds > 65536) return LH_ERR_UNSUPPORTED;
   P.lds_bytes = (int)lds;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   dim3 grid(P.T, B * H);
   if (tie_mode == LH_TIE_REFERENCE)
-    hipLaunchKernelGGL(select_kernel<LH_TIE_REFERENCE>, grid, dim3(64), P.lds_bytes, st, scores_qk, scores_kq,
+    hipLaunchKernelGGL(select_kernel<LH_TIE_REFERENCE>, grid, dim3(256), P.lds_bytes, st, scores_qk, scores_kq,
                        indices, inverse, P);
   else
-    hipLaunchKernelGGL(select_kernel<LH_TIE_LOWER_INDEX>, grid, dim3(64), P.lds_bytes, st, scores_qk, scores_kq,
+    hipLaunchKernelGGL(select_kernel<LH_TIE_LOWER_INDEX>, grid, dim3(256), P.lds_bytes, st, scores_qk, scores_kq,
                        indices, inverse, P);
   LH_CHECK_LAUNCH();
   return LH_OK;
