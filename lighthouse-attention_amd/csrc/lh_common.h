@@ -48,6 +48,16 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 }
 
 // ---------------------------------------------------------------------------
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own L2.
+// Logical block of dispatch index w: each XCD gets a contiguous run, so
+// neighbouring rows that read the same inputs (pooled rows shared by a span of
+// tokens) share an L2.  Identity when the grid is not a multiple of 8.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ long long xcd_block(long long w, long long total) {
+  return (total & 7) ? w : (w & 7) * (total >> 3) + (w >> 3);
+}
+
+// ---------------------------------------------------------------------------
 // Rotary embedding of 8 consecutive elements of a row (pairs j = 0..3 are
 // (f[2j], f[2j+1])) by the angles whose (cos, sin) pairs are c01 = (c0, s0, c1, s1)
 // and c23 = (c2, s2, c3, s3).  FWD rotates by +theta (torchtitan's

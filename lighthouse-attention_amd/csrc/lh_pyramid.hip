@@ -190,7 +190,7 @@ struct PyrBwdArgs {
 template <int NL, bool ROPE>
 __global__ __launch_bounds__(256) void pyramid_bwd_kernel(const PyrBwdArgs a) {
   const int tid = threadIdx.x;
-  const long long row = (long long)blockIdx.x * 16 + (tid >> 4);
+  const long long row = xcd_block(blockIdx.x, gridDim.x) * 16 + (tid >> 4);  // a span's rows on one L2
   const int l16 = tid & 15;
   if (row >= a.rows) return;
   const int h = (int)(row % a.H);

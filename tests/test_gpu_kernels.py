@@ -137,6 +137,36 @@ def test_attention_fwd_bwd_gathered(pkg, dev, S, L, p, k, H):
     assert_close(dv, v.grad, "dv")
 
 
+@pytest.mark.parametrize("n,B,H", [(8, 1, 2), (17, 2, 1), (100, 1, 3), (333, 2, 2)])
+def test_attention_gathered_ragged(pkg, dev, n, B, H):
+    """Explicit row maps (random distinct rows of the base and pooled tensors,
+    in random order) at lengths that leave partial tiles and partial index
+    groups: the gathered-row copies of every kernel, forward and backward."""
+    S, Sp = 640, 160
+    print(f"gathered attention n={n} B={B} H={H}", flush=True)
+    cpu, gpu = _bf16_inputs((B, S, H, 128), 3, 40 + n, dev)
+    pcpu, pgpu = _bf16_inputs((B, Sp, H, 128), 3, 50 + n, dev)
+    g = torch.Generator().manual_seed(n)
+    idx = torch.stack([torch.stack([torch.randperm(S + Sp, generator=g)[:n] for _ in range(H)]) for _ in range(B)])
+    idx = idx.int()
+    x, px = gpu[0], pgpu[0]
+    rows = pkg._native.Rows(*gpu, (x.stride(0), x.stride(1), x.stride(2)), *pgpu,
+                            (px.stride(0), px.stride(1), px.stride(2)), split=S)
+    o, lse = pkg._native.attn_fwd(rows, idx.to(dev), B, H, n)
+    gi = idx.long()[..., None].expand(-1, -1, -1, 128)
+    sel = [torch.gather(torch.cat([c, p], 1).float().transpose(1, 2), 2, gi) for c, p in zip(cpu, pcpu)]
+    q, k, v = [s.clone().requires_grad_() for s in sel]
+    ref = O.sdpa_causal(q, k, v)
+    assert_close(o, ref, "gathered attention out")
+    do = torch.randn(B, H, n, 128, generator=g).bfloat16()
+    ref.backward(do.float())
+    delta = (do.float() * o.float().cpu()).sum(-1).to(dev)
+    dq, dk, dv = pkg._native.attn_bwd(rows, idx.to(dev), B, H, n, do.to(dev), lse, delta)
+    assert_close(dq, q.grad, "gathered dq")
+    assert_close(dk, k.grad, "gathered dk")
+    assert_close(dv, v.grad, "gathered dv")
+
+
 @pytest.mark.parametrize("n", [1000, 64, 200])
 def test_attention_dense_ragged(pkg, dev, n):
     """Identity row map, lengths not a multiple of the 128-row block."""
