@@ -42,7 +42,7 @@ constexpr int BMK = 128;  // keys per workgroup of the key-stationary kernel: 4 
 constexpr int QW = 8;     // waves per workgroup of the query-stationary kernels (32 queries each)
 constexpr int BN = 64;   // rows per LDS tile
 constexpr float RESCALE_LOG2 = 8.0f;
-constexpr int FWD_AHEAD = 8;  // forward: LDS operands read this many MFMAs ahead
+constexpr int FWD_AHEAD = 4;  // forward: LDS operands read this many MFMAs ahead
 constexpr int DQ_AHEAD = 8;   // dQ kernel, S and dP products
 constexpr int DQ_AHEAD2 = 4;  // dQ kernel, dS K product
 
