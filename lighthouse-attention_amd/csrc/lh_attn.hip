@@ -165,7 +165,10 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // vector-memory counter only; every caller waits for it explicitly (wait_vm,
 // wait_loads) before a barrier publishes the data.  Loads the compiler does
 // know about stay correctly waited: the counter completes in order, so an
-// extra untracked load only makes the compiler's counts conservative.
+// extra untracked load only makes the compiler's counts conservative.  M0 is
+// a reserved register that the compiler may assume unchanged across inline
+// assembly; no compiler-generated instruction of this file uses it (checked
+// on the generated gfx950 assembly by tests/test_isa.py).
 __device__ __forceinline__ void g2l16(const bf16_t* g, bf16_t* lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr(lds_base))
                : "memory", "m0");
@@ -224,31 +227,22 @@ __device__ __forceinline__ void issue_dense(bf16_t* tile, const bf16_t* base, in
 // every direct load of this wave has landed in LDS
 __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0); }
 
-// A operand from tile row r: d = 16c + 8hh .. 16c + 8hh + 7
-__device__ __forceinline__ u32x4 op_row(const bf16_t* tile, int r, int c, int hh) {
-  return *reinterpret_cast<const u32x4*>(tile + r * LH_D + (((2 * c + hh) ^ swz(r)) << 3));
-}
-
-// A operand of X^T: column d = 32db + lane%32; k-slots u are rows
-// r0 + 8(u/4) + 4(lane/32) + u%4 (r0 a multiple of 16).  Within each 16-lane
-// group, ds_read_b64_tr_b16 returns to lane i, element e, the 16-bit word i%4 of
-// the 8 bytes addressed by lane i/4 + 4e; each lane therefore addresses 4
-// columns of one row of a 4-row x 16-column block.
-__device__ __forceinline__ u32x4 op_tr(const bf16_t* tile, int r0, int db, int lane) {
-  const int g = lane >> 4, j = lane & 15;
-  const int r = r0 + 4 * (lane >> 5) + (j >> 2);
-  const int ch = 4 * db + 2 * (g & 1) + ((j & 3) >> 1);
-  const int sub = (j & 1) << 2;
-  const u32x2 lo = ld_tr16(tile + r * LH_D + ((ch ^ swz(r)) << 3) + sub);
-  const u32x2 hi = ld_tr16(tile + (r + 8) * LH_D + ((ch ^ swz(r + 8)) << 3) + sub);
-  return u32x4{lo.x, lo.y, hi.x, hi.y};
-}
+// MFMA A operands read from a tile (the plain forms of lds_row / lds_tr below):
+//   row operand of tile row r, k-slice c, lane half hh (d = 16c + 8hh .. +7):
+//     the 16 bytes at element r * 128 + (((2c + hh) ^ swz(r)) << 3);
+//   transposed operand of X^T, column d = 32 db + lane % 32, k-slots u = rows
+//     r0 + 8 (u / 4) + 4 (lane / 32) + u % 4 (r0 a multiple of 16): within each
+//     16-lane group, ds_read_b64_tr_b16 returns to lane i, element e, the 16-bit
+//     word i % 4 of the 8 bytes addressed by lane i / 4 + 4e, so lane (g, j)
+//     (g = lane / 16, j = lane % 16) reads row r = r0 + 4 (lane / 32) + j / 4,
+//     chunk ch = 4 db + 2 (g & 1) + (j & 3) / 2, sub-word offset 4 (j & 1), and
+//     the same at row r + 8 for the operand's upper half.
 
 // Lane-constant parts of the operand addresses above, as byte offsets inside
 // a 16 KB tile, arranged so that a k-slice / column block is folded in with
 // one XOR:
-//   op_row(tile, r, c, hh)            at row ^ (c << 5), + 8192 for rows 32..63
-//   op_tr(tile, r0, db, lane) lo / hi at tr0 ^ (db << 6) and tr1 ^ (db << 6), + 256 r0
+//   row operand (r, c, hh)             at row ^ (c << 5), + 8192 for rows 32..63
+//   transposed operand (r0, db) lo / hi at tr0 ^ (db << 6) and tr1 ^ (db << 6), + 256 r0
 // (the chunk swizzle is an XOR, and 2c + hh = 2c ^ hh, 4 db + C = 4 db ^ C).
 // Recomputing the few XORs per tile keeps the addresses out of long-lived registers.
 struct LaneLds {
@@ -265,13 +259,13 @@ __device__ __forceinline__ LaneLds lane_lds(int lane) {
   return o;
 }
 
-// op_row of tile rows 32 qb + lane%32, k-slice c
+// row operand of tile rows 32 qb + lane%32, k-slice c
 __device__ __forceinline__ u32x4 lds_row(const bf16_t* tile, const LaneLds& ll, int qb, int c) {
   return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(tile) + ((ll.row ^ ((uint32_t)c << 5)) +
                                                                                  8192u * qb));
 }
 
-// op_tr of tile rows r0 .., column block db
+// transposed operand of tile rows r0 .., column block db
 __device__ __forceinline__ u32x4 lds_tr(const bf16_t* tile, const LaneLds& ll, int r0, int db) {
   const char* t = reinterpret_cast<const char*>(tile);
   const uint32_t x = (uint32_t)db << 6, o = 256u * r0;
