@@ -180,9 +180,14 @@ struct PyrBwdArgs {
   int B, S, H, L, shift, S_tot;
   int off[9], len[9];
   long long rows;
+  int chunks;  // 16-token chunks per (b, h)
 };
 
-// One 16-lane group per (b, t, h) row, 8 d each.  All levels' inverse lookups
+// One 16-lane group per (b, t, h) row, 8 d each; a block covers 16 consecutive
+// tokens of one (b, h), so the rows of a pooled node spanning up to 16 tokens
+// are read by one block (the wave or block coalesces the repeats instead of
+// several blocks fetching the row through L2), and consecutive chunks of a head
+// stay on one XCD (`xcd_block`).  All levels' inverse lookups
 // are issued first, then all gradient-row loads, so a row costs two dependent
 // memory round trips instead of two per level.  ROPE: the q and k sums are
 // the gradients of rotated rows; they are rotated back (the adjoint of the
@@ -190,13 +195,13 @@ struct PyrBwdArgs {
 template <int NL, bool ROPE>
 __global__ __launch_bounds__(256) void pyramid_bwd_kernel(const PyrBwdArgs a) {
   const int tid = threadIdx.x;
-  const long long row = xcd_block(blockIdx.x, gridDim.x) * 16 + (tid >> 4);  // a span's rows on one L2
+  const long long blk = xcd_block(blockIdx.x, gridDim.x);
+  const long long bh = blk / a.chunks;
+  const int t = (int)(blk - bh * a.chunks) * 16 + (tid >> 4);
   const int l16 = tid & 15;
-  if (row >= a.rows) return;
-  const int h = (int)(row % a.H);
-  const long long bt = row / a.H;
-  const int t = (int)(bt % a.S);
-  const int b = (int)(bt / a.S);
+  if (t >= a.S) return;
+  const int h = (int)(bh % a.H);
+  const int b = (int)(bh / a.H);
   const size_t irow = (size_t)(b * a.H + h) * a.S_tot;
   const int64_t gbase = (int64_t)b * a.gb + (int64_t)h * a.gh + 8 * l16;
   int s[NL];
@@ -344,7 +349,8 @@ int pyramid_bwd_impl(const void* gq, const void* gk, const void* gv, int64_t gb,
   a.B = B; a.S = S; a.H = H; a.L = L; a.shift = shift; a.S_tot = g.total;
   for (int l = 1; l <= L; ++l) { a.off[l] = g.off[l]; a.len[l] = g.len[l]; }
   a.rows = (long long)B * S * H;
-  const long long blocks = (a.rows + 15) / 16;
+  a.chunks = (S + 15) / 16;
+  const long long blocks = (long long)B * H * a.chunks;
   if (blocks > 2147483647LL) return LH_ERR_UNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (freqs)
