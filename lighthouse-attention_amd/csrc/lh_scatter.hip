@@ -62,7 +62,7 @@ __global__ __launch_bounds__(256) void scatter_fwd_kernel(const ScatArgs a) {
   *reinterpret_cast<uint4*>(a.dst + b * a.sb + h * a.sh + t * a.st + 8 * l16) = pack8(acc);
 }
 
-// Backward: the span's dout rows are loaded four at a time (independent
+// Backward: the span's dout rows are loaded eight at a time (independent
 // loads), and the attention-output row for delta is loaded up front.
 __global__ __launch_bounds__(256) void scatter_bwd_kernel(const ScatArgs a) {
   const int tid = threadIdx.x;
@@ -84,12 +84,12 @@ __global__ __launch_bounds__(256) void scatter_bwd_kernel(const ScatArgs a) {
     const int stop = min(start + c, a.S_out);
     const int b = (int)(bh / a.H), h = (int)(bh % a.H);
     const bf16_t* src = a.src + b * a.sb + h * a.sh + 8 * l16;
-    for (int t = start; t < stop; t += 4) {
-      uint4 v[4];
+    for (int t = start; t < stop; t += 8) {
+      uint4 v[8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = t + u < stop ? ld16(src + (t + u) * a.st) : make_uint4(0, 0, 0, 0);
+      for (int u = 0; u < 8; ++u) v[u] = t + u < stop ? ld16(src + (t + u) * a.st) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 8; ++u) {
         if (t + u >= stop) break;  // same left-to-right fp32 sum as one row at a time
         float f[8];
         unpack8(v[u], f);
