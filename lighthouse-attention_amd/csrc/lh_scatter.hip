@@ -28,38 +28,55 @@ struct ScatArgs {
 
 __device__ __forceinline__ uint4 ld16(const bf16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
-// Forward: all levels' inverse lookups first, then all row loads (two
-// dependent memory round trips per output row instead of two per level).
-template <int NL>
+// Forward: each 16-lane group owns SF_ROWS output rows (16 apart); all their
+// levels' inverse lookups are issued first, then all row loads, so a group
+// has SF_ROWS * NL loads in flight across two dependent round trips.
+constexpr int SF_ROWS = 2;
+template <int NL, int R>
 __global__ __launch_bounds__(256) void scatter_fwd_kernel(const ScatArgs a) {
   const int tid = threadIdx.x;
-  const long long row = (long long)blockIdx.x * 16 + (tid >> 4);
   const int l16 = tid & 15;
-  if (row >= a.rows) return;
-  const int t = (int)(row % a.S_out);
-  const long long bh = row / a.S_out;
-  const int32_t* inv = a.map + bh * a.S_tot;
-  const bf16_t* src = a.src + (size_t)bh * a.n * LH_D + 8 * l16;
-  int s[NL];
+  const long long row0 = (long long)blockIdx.x * (16 * R) + (tid >> 4);
+  int s[R][NL], tr[R];
+  long long bhr[R];
 #pragma unroll
-  for (int l = 0; l < NL; ++l) {
-    const int node = ((t + 1) >> (l * a.shift)) - 1;
-    s[l] = (node >= 0 && node < a.len[l + 1]) ? inv[a.off[l + 1] + node] : -1;
+  for (int r = 0; r < R; ++r) {
+    const long long row = row0 + 16 * r;
+    const bool ok = row < a.rows;
+    const long long bh = ok ? row / a.S_out : 0;
+    const int t = ok ? (int)(row - bh * a.S_out) : 0;
+    tr[r] = ok ? t : -1;
+    bhr[r] = bh;
+    const int32_t* inv = a.map + bh * a.S_tot;
+#pragma unroll
+    for (int l = 0; l < NL; ++l) {
+      const int node = ((t + 1) >> (l * a.shift)) - 1;
+      s[r][l] = (ok && node >= 0 && node < a.len[l + 1]) ? inv[a.off[l + 1] + node] : -1;
+    }
   }
-  uint4 v[NL];
+  uint4 v[R][NL];
 #pragma unroll
-  for (int l = 0; l < NL; ++l) v[l] = s[l] >= 0 ? ld16(src + (size_t)s[l] * LH_D) : make_uint4(0, 0, 0, 0);
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int r = 0; r < R; ++r) {
+    const bf16_t* src = a.src + (size_t)bhr[r] * a.n * LH_D + 8 * l16;
 #pragma unroll
-  for (int l = 0; l < NL; ++l) {
-    if (s[l] < 0) continue;  // keeps the fp32 sum of exactly the present terms
-    float f[8];
-    unpack8(v[l], f);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += f[e];
+    for (int l = 0; l < NL; ++l)
+      v[r][l] = s[r][l] >= 0 ? ld16(src + (size_t)s[r][l] * LH_D) : make_uint4(0, 0, 0, 0);
   }
-  const int b = (int)(bh / a.H), h = (int)(bh % a.H);
-  *reinterpret_cast<uint4*>(a.dst + b * a.sb + h * a.sh + t * a.st + 8 * l16) = pack8(acc);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (tr[r] < 0) continue;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int l = 0; l < NL; ++l) {
+      if (s[r][l] < 0) continue;  // keeps the fp32 sum of exactly the present terms
+      float f[8];
+      unpack8(v[r][l], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += f[e];
+    }
+    const int b = (int)(bhr[r] / a.H), h = (int)(bhr[r] % a.H);
+    *reinterpret_cast<uint4*>(a.dst + b * a.sb + h * a.sh + (int64_t)tr[r] * a.st + 8 * l16) = pack8(acc);
+  }
 }
 
 // Backward: the span's dout rows are loaded eight at a time (independent
@@ -136,19 +153,19 @@ extern "C" int lh_scatter_fwd(const void* attn, const int32_t* inverse, void* ou
   if (rc) return rc;
   a.src = (const bf16_t*)attn; a.map = inverse; a.dst = (bf16_t*)out;
   a.rows = (long long)B * H * S_out;
-  const long long blocks = (a.rows + 15) / 16;
+  const long long blocks = (a.rows + 16 * SF_ROWS - 1) / (16 * SF_ROWS);
   if (blocks > 2147483647LL) return LH_ERR_UNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)blocks), blk(256);
   switch (L) {
-    case 1: hipLaunchKernelGGL(scatter_fwd_kernel<1>, grid, blk, 0, st, a); break;
-    case 2: hipLaunchKernelGGL(scatter_fwd_kernel<2>, grid, blk, 0, st, a); break;
-    case 3: hipLaunchKernelGGL(scatter_fwd_kernel<3>, grid, blk, 0, st, a); break;
-    case 4: hipLaunchKernelGGL(scatter_fwd_kernel<4>, grid, blk, 0, st, a); break;
-    case 5: hipLaunchKernelGGL(scatter_fwd_kernel<5>, grid, blk, 0, st, a); break;
-    case 6: hipLaunchKernelGGL(scatter_fwd_kernel<6>, grid, blk, 0, st, a); break;
-    case 7: hipLaunchKernelGGL(scatter_fwd_kernel<7>, grid, blk, 0, st, a); break;
-    default: hipLaunchKernelGGL(scatter_fwd_kernel<8>, grid, blk, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((scatter_fwd_kernel<1, SF_ROWS>), grid, blk, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((scatter_fwd_kernel<2, SF_ROWS>), grid, blk, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((scatter_fwd_kernel<3, SF_ROWS>), grid, blk, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((scatter_fwd_kernel<4, SF_ROWS>), grid, blk, 0, st, a); break;
+    case 5: hipLaunchKernelGGL((scatter_fwd_kernel<5, SF_ROWS>), grid, blk, 0, st, a); break;
+    case 6: hipLaunchKernelGGL((scatter_fwd_kernel<6, SF_ROWS>), grid, blk, 0, st, a); break;
+    case 7: hipLaunchKernelGGL((scatter_fwd_kernel<7, SF_ROWS>), grid, blk, 0, st, a); break;
+    default: hipLaunchKernelGGL((scatter_fwd_kernel<8, SF_ROWS>), grid, blk, 0, st, a); break;
   }
   LH_CHECK_LAUNCH();
   return LH_OK;
