@@ -280,25 +280,62 @@ def run_model(args, pkg, torch):
             "native_ms_per_step": round(native_ms, 3), "final_loss": round(loss.item(), 4)}
 
 
+def _cpu_model():
+    """Host CPU model name (lscpu's "Model name"), or None."""
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, ValueError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def run_cpu_baseline(args, torch):
-    """CPU oracle (fp32, reference path restated) on a bounded sample: the same
-    workload with `--cpu-heads` of its H heads (all of them for the norm scorer,
-    about 10 s on 16 cores), scaled to all heads."""
-    import numpy as np
+    """CPU oracle (fp32, the reference path restated) on a bounded sample: the same
+    workload with `--cpu-heads` of its H heads (2 for the norm scorer, 1 for the
+    dilated one), scaled to all heads.  One warm-up run, then the median of
+    `--cpu-runs` timed runs each of the forward alone and of forward + backward."""
+    import statistics
     from oracle import lh_oracle as O
     w = WORKLOADS[args.workload]
     B, H, S, L, p, k, strict = (w[n] for n in ("B", "H", "S", "L", "p", "topk", "strict"))
-    hs = max(1, min(args.cpu_heads if args.cpu_heads else (1 if w["scorer"] == "dilated" else H), H))
-    xs, dout = make_inputs(w, torch, torch.device("cpu"), seed=99, heads=list(range(hs)))
-    xs = [x.float().requires_grad_() for x in xs]
-    t0 = time.perf_counter()
-    out, idx = O.lighthouse_layer(*xs, L, p, k, scorer=w["scorer"], dilation=w.get("dilation", 4), strict=strict)
-    out.backward(dout.float())
-    dt = time.perf_counter() - t0
-    tok_s = B * S / (dt * H / hs)
-    return {"value": round(tok_s, 2), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"oracle layer fwd+bwd fp32 on {hs} of {H} heads (B={B}, S={S}), {dt:.1f} s, "
-                      f"scaled x{H // hs} to all heads"}
+    hs = max(1, min(args.cpu_heads if args.cpu_heads else (1 if w["scorer"] == "dilated" else 2), H))
+    xs0, dout = make_inputs(w, torch, torch.device("cpu"), seed=99, heads=list(range(hs)))
+    dout = dout.float()
+
+    def run(backward):
+        xs = [x.float().requires_grad_(backward) for x in xs0]
+        t0 = time.perf_counter()
+        out, _ = O.lighthouse_layer(*xs, L, p, k, scorer=w["scorer"], dilation=w.get("dilation", 4), strict=strict)
+        if backward:
+            out.backward(dout)
+        return time.perf_counter() - t0
+
+    run(True)  # warm-up
+    t_fb = statistics.median(run(True) for _ in range(args.cpu_runs))
+    with torch.no_grad():
+        t_f = statistics.median(run(False) for _ in range(args.cpu_runs))
+    scale = H / hs
+    tok = lambda t: round(B * S / (t * scale), 2)  # noqa: E731
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count()
+    return {"value": tok(t_fb), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "fwd_value": tok(t_f), "nproc": nproc, "cpu_model": _cpu_model(),
+            "sample": f"oracle layer fp32 on {hs} of {H} heads (B={B}, S={S}): 1 warm-up, median of "
+                      f"{args.cpu_runs} runs, fwd+bwd {t_fb:.2f} s, fwd {t_f:.2f} s; scaled x{H // hs} to all "
+                      "heads; value = fwd+bwd, fwd_value = fwd only"}
 
 
 def main():
@@ -308,7 +345,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS) + sorted(MODEL_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=0, help="heads in the CPU sample (0: all, or 1 for dilated)")
+    ap.add_argument("--cpu-heads", type=int, default=0,
+                    help="heads in the CPU sample (0: 2 for the norm scorer, 1 for the dilated one)")
+    ap.add_argument("--cpu-runs", type=int, default=3, help="timed CPU runs per figure (median reported)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB five times (reference kernel of known "
                          "traffic for the FETCH_SIZE / WRITE_SIZE counters) and exit")

@@ -130,9 +130,26 @@ int lh_select_topk(const float *scores_qk, const float *scores_kq,
 /*
  * inverse[b,h,r] = s where indices[b,h,s] == r, else -1.  (Device helper for
  * callers holding only `indices`, e.g. scatter_to_base_sequence.)
+ * Entries outside [0, S_tot) are skipped.  Indices must be unique per (b, h):
+ * for a row named twice, one of its positions (unspecified which) is kept, so
+ * the fan-out and its adjoint would count that row once.  lh_check_indices
+ * detects duplicates.
  */
 int lh_build_inverse(const int32_t *indices, int n, int32_t *inverse, int S_tot,
                      int B, int H, void *stream);
+
+/*
+ * Validation of an index array, for callers' debug/check modes (no counterpart
+ * in the reference, whose Python asserts shapes only).
+ *   indices  int32 [B, H, n] contiguous
+ *   counts   device int32[2], written: counts[0] = entries outside [lo, hi),
+ *            counts[1] = duplicate entries within a (b, h) (0 unless marks given;
+ *            with lo = -1, entries equal to -1 are empty slots, never duplicates)
+ *   marks    device int32 [B, H, hi - lo] workspace for the duplicate count, or NULL
+ * Asynchronous like every entry point: read `counts` after the stream has run.
+ */
+int lh_check_indices(const int32_t *indices, int B, int H, int n, int lo, int hi,
+                     int32_t *marks, int32_t *counts, void *stream);
 
 /*
  * Causal attention over gathered rows, forward.
@@ -142,6 +159,9 @@ int lh_build_inverse(const int32_t *indices, int n, int32_t *inverse, int S_tot,
  *   base + b*sb + r*ss + h*sh            if r <  split
  *   pool + b*pb + (r-split)*ps + h*ph    if r >= split
  * where r = indices[b,h,s] (or r = s when indices == NULL).
+ * Precondition (not checked on the device): 0 <= indices[b,h,s] < split + P,
+ * P the number of pooled rows behind `pool` (S_tot - S for a pyramid); the
+ * kernels read row r unguarded.  lh_check_indices validates an index array.
  *   out  bf16 [B, H, n, D];  lse fp32 [B, H, n] (log2-domain: m*log2(e)+log2(sum))
  */
 int lh_attn_fwd(const void *q, const void *k, const void *v, int64_t sb, int64_t ss, int64_t sh,
@@ -156,7 +176,7 @@ int lh_attn_fwd(const void *q, const void *k, const void *v, int64_t sb, int64_t
  *   dout   bf16 [B, H, n, D] (from lh_scatter_bwd); lse, delta fp32 [B, H, n]
  *   dq, dk, dv bf16 [B, H, n, D] in selected order
  * With indices, n must be >= 8 (LH_ERR_UNSUPPORTED otherwise); every selected
- * length of a Lighthouse pyramid is.
+ * length of a Lighthouse pyramid is.  Index precondition as lh_attn_fwd.
  */
 int lh_attn_bwd(const void *q, const void *k, const void *v, int64_t sb, int64_t ss, int64_t sh,
                 const void *qp, const void *kp, const void *vp, int64_t pb, int64_t ps, int64_t ph,
@@ -185,7 +205,10 @@ int lh_attn_bwd_dq(const void *q, const void *k, const void *v, int64_t sb, int6
  * out[b,h,t] = sum over levels l of attn[b,h,inverse[b,h,off_l + (t+1)/c_l - 1]].
  * Replaces _scatter_fanout_fwd_kernel / _ScatterToBaseAutograd.forward
  * (src/lighthouse_selection.py:408-459, :519-550) without atomics.
- *   attn bf16 [B, H, n, D]; out bf16 [B, H, S_out, D] logically (rows >= S are zero),
+ *   attn bf16 [B, H, n, D]; out bf16 [B, H, S_out, D] logically.  When S_out > S, a row
+ *   t >= S receives the coarse-level entries whose span [(i+1)c_l - 1, (i+2)c_l - 2]
+ *   reaches t (as in the reference); rows no span reaches are zero.  `inverse` entries
+ *   must be -1 or < n.  Layout:
  *   element (b, h, t, :) at out + b*ob + h*oh + t*os (D contiguous): (H*S_out*D, S_out*D, D)
  *   for [B, H, S_out, D] storage, (S_out*H*D, D, H*D) for [B, S_out, H, D] storage.
  */

@@ -41,6 +41,7 @@ _SIGS = {
     "lh_dilated_scores": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "lh_select_topk": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_build_inverse": (_I, [_P, _I, _P, _I, _I, _I, _P]),
+    "lh_check_indices": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "lh_attn_fwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _I, _P,
                          _I, _I, _I, _I, _F, _P, _P, _P]),
     "lh_attn_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _I, _P,
@@ -117,6 +118,57 @@ def _need_gpu(*ts):
     for t in ts:
         if t is not None and not t.is_cuda:
             raise LighthouseHipError("lighthouse_hip kernels need GPU tensors (no CPU path)")
+
+
+def _need_rows(what, *ts):
+    """bf16 storage with a contiguous last (head) dimension: what every row-reading
+    kernel of the library assumes."""
+    for t in ts:
+        if t is None:
+            continue
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{what}: the native kernels read and write bfloat16 rows; got {t.dtype}")
+        if t.dim() and t.stride(-1) != 1:
+            raise ValueError(f"{what}: the head dimension must be contiguous (stride(-1) == 1)")
+
+
+def _need_dtype(what, dtype, *ts):
+    for t in ts:
+        if t is not None and t.dtype != dtype:
+            raise TypeError(f"{what}: expected {dtype}, got {t.dtype}")
+
+
+# Index validation before every launch that reads caller indices: off by default,
+# on with LH_CHECK_INDICES=1 in the environment or set_check_indices(True).  Each
+# check synchronizes the stream (debug aid, not for timed runs).
+_check_indices = os.environ.get("LH_CHECK_INDICES", "0") not in ("", "0")
+
+
+def set_check_indices(on: bool) -> bool:
+    """Turn the index check mode on or off; returns the previous setting."""
+    global _check_indices
+    prev, _check_indices = _check_indices, bool(on)
+    return prev
+
+
+def check_indices(indices, lo: int, hi: int, unique: bool = True, what: str = "indices"):
+    """Raise ``IndexError`` unless every entry of ``indices`` [B, H, n] lies in
+    ``[lo, hi)`` and (``unique``) no (b, h) names a row twice.  Synchronizes."""
+    _need_gpu(indices)
+    _need_dtype(what, torch.int32, indices)
+    idx = indices.contiguous()
+    B, H, n = idx.shape
+    dev = idx.device
+    counts = torch.empty(2, dtype=torch.int32, device=dev)
+    marks = torch.empty(B, H, hi - lo, dtype=torch.int32, device=dev) if unique else None
+    with torch.cuda.device(dev):
+        rc = lib().lh_check_indices(_ptr(idx), B, H, n, lo, hi, _ptr(marks), _ptr(counts), _stream(dev))
+    _check(rc, "lh_check_indices")
+    bad, dup = (int(c) for c in counts.cpu())
+    if bad:
+        raise IndexError(f"{what}: {bad} entries outside [{lo}, {hi})")
+    if dup:
+        raise IndexError(f"{what}: {dup} duplicate entries (indices must be unique per (batch, head))")
 
 
 def geometry(S: int, L: int, p: int, topk: int, strict: bool = True):
@@ -257,10 +309,14 @@ def select_topk(scores_qk, scores_kq, S: int, L: int, p: int, topk: int, tie: st
     return idx, inv
 
 
-def build_inverse(indices, S_tot: int):
+def build_inverse(indices, S_tot: int, validate: bool = False):
+    """Inverse map of ``indices`` [B, H, n]; with ``validate`` (or the check mode)
+    the indices are first checked to lie in [0, S_tot) and be unique per (b, h)."""
+    _need_dtype("build_inverse indices", torch.int32, indices)
     _need_gpu(indices)
+    if validate or _check_indices:
+        check_indices(indices, 0, S_tot, unique=True, what="indices")
     idx = indices.contiguous()
-    assert idx.dtype == torch.int32
     B, H, n = idx.shape
     inv = torch.empty(B, H, S_tot, dtype=torch.int32, device=idx.device)
     with torch.cuda.device(idx.device):
@@ -273,23 +329,41 @@ class Rows:
     """Where row r of (b, h) lives: ``base`` [.., r, .., D] for r < split,
     else ``pool`` at r - split.  Strides are in elements, D contiguous."""
 
-    def __init__(self, q, k, v, base_strides, qp=None, kp=None, vp=None, pool_strides=(0, 0, 0), split=None):
+    def __init__(self, q, k, v, base_strides, qp=None, kp=None, vp=None, pool_strides=(0, 0, 0), split=None,
+                 limit=None):
+        _need_rows("attention rows", q, k, v, qp, kp, vp)
         self.q, self.k, self.v = q, k, v
         self.qp, self.kp, self.vp = qp, kp, vp
         self.bs = tuple(int(s) for s in base_strides)
         self.ps = tuple(int(s) for s in pool_strides)
         self.split = int(split) if split is not None else 2 ** 31 - 1
+        # number of addressable rows (split + pooled rows), for the index check mode
+        self.limit = int(limit) if limit is not None else None
+
+    def check(self, indices):
+        if _check_indices and indices is not None and self.limit is not None:
+            check_indices(indices, 0, self.limit, unique=False, what="attention row indices")
 
     def args(self):
         return (_ptr(self.q), _ptr(self.k), _ptr(self.v), *self.bs,
                 _ptr(self.qp), _ptr(self.kp), _ptr(self.vp), *self.ps, self.split)
 
 
+def _bwd_args_check(rows, indices, dout, lse, delta):
+    _need_dtype("attention backward indices", torch.int32, indices)
+    _need_rows("attention backward dout", dout)
+    _need_dtype("attention backward lse/delta", torch.float32, lse, delta)
+    _need_gpu(rows.q, dout, lse, delta, indices)
+    rows.check(indices)
+
+
 def attn_fwd(rows: Rows, indices, B: int, H: int, n: int, D: int = D_SUPPORTED, scale: float | None = None):
     """Causal attention over the rows named by ``indices`` [B, H, n] (None = identity).
 
     Returns ``(O bf16 [B, H, n, D], lse fp32 [B, H, n])`` (lse in the exp2 domain)."""
+    _need_dtype("attn_fwd indices", torch.int32, indices)
     _need_gpu(rows.q, indices)
+    rows.check(indices)
     dev = rows.q.device
     scale = D ** -0.5 if scale is None else scale
     idx = indices.contiguous() if indices is not None else None
@@ -304,7 +378,7 @@ def attn_fwd(rows: Rows, indices, B: int, H: int, n: int, D: int = D_SUPPORTED, 
 def attn_bwd_dkdv(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D: int = D_SUPPORTED,
                   scale: float | None = None):
     """dK, dV of the gathered rows (key-stationary kernel): two bf16 [B, H, n, D]."""
-    _need_gpu(rows.q, dout)
+    _bwd_args_check(rows, indices, dout, lse, delta)
     dev = rows.q.device
     scale = D ** -0.5 if scale is None else scale
     idx = indices.contiguous() if indices is not None else None
@@ -319,7 +393,7 @@ def attn_bwd_dkdv(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta,
 def attn_bwd_dq(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D: int = D_SUPPORTED,
                 scale: float | None = None):
     """dQ of the gathered rows (query-stationary kernel): bf16 [B, H, n, D]."""
-    _need_gpu(rows.q, dout)
+    _bwd_args_check(rows, indices, dout, lse, delta)
     dev = rows.q.device
     scale = D ** -0.5 if scale is None else scale
     idx = indices.contiguous() if indices is not None else None
@@ -334,7 +408,7 @@ def attn_bwd_dq(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D
 def attn_bwd(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D: int = D_SUPPORTED,
              scale: float | None = None):
     """Gradients w.r.t. the gathered q, k, v rows: three bf16 [B, H, n, D]."""
-    _need_gpu(rows.q, dout)
+    _bwd_args_check(rows, indices, dout, lse, delta)
     dev = rows.q.device
     scale = D ** -0.5 if scale is None else scale
     idx = indices.contiguous() if indices is not None else None
@@ -352,9 +426,13 @@ def scatter_fwd(attn, inverse, S: int, S_out: int, L: int, p: int, seq_major: bo
 
     ``seq_major`` stores the result as ``[B, S_out, H, D]`` and returns its
     ``[B, H, S_out, D]`` view (transposing it back is then free)."""
+    _need_rows("scatter_fwd attn", attn)
+    _need_dtype("scatter_fwd inverse", torch.int32, inverse)
     _need_gpu(attn, inverse)
     attn = attn.contiguous()
     B, H, n, D = attn.shape
+    if _check_indices:
+        check_indices(inverse, -1, n, unique=False, what="scatter_fwd inverse map")
     if seq_major:
         out = torch.empty(B, S_out, H, D, dtype=attn.dtype, device=attn.device).transpose(1, 2)
     else:
@@ -370,7 +448,11 @@ def scatter_fwd(attn, inverse, S: int, S_out: int, L: int, p: int, seq_major: bo
 def scatter_bwd(dout, indices, o, S: int, L: int, p: int):
     """``(dattn bf16 [B, H, n, D], delta fp32 [B, H, n] or None)``; ``dout`` may have
     any (batch, head, seq) strides with D contiguous."""
-    _need_gpu(dout, indices)
+    _need_rows("scatter_bwd", dout, o)
+    _need_dtype("scatter_bwd indices", torch.int32, indices)
+    _need_gpu(dout, indices, o)
+    if _check_indices:
+        check_indices(indices, 0, pyramid_lengths(S, L, p)[2], unique=True, what="scatter_bwd indices")
     if dout.stride(3) != 1 or any(st % 8 for st in dout.stride()[:3]) or dout.data_ptr() % 16:
         dout = dout.contiguous()
     B, H, S_out, D = dout.shape
@@ -389,8 +471,12 @@ def scatter_bwd(dout, indices, o, S: int, L: int, p: int):
 def pyramid_bwd(gq, gk, gv, inverse, B: int, S: int, H: int, L: int, p: int, D: int = D_SUPPORTED):
     """Base-row gradients bf16 [B, S, H, D] from selected-space (or pyramid-row) grads
     ``g*`` indexed [b, h, s, :] with any strides (D contiguous)."""
+    _need_rows("pyramid_bwd grads", gq, gk, gv)
+    _need_dtype("pyramid_bwd inverse", torch.int32, inverse)
     ref = next(g for g in (gq, gk, gv) if g is not None)
-    _need_gpu(ref)
+    _need_gpu(ref, inverse)
+    if _check_indices and inverse is not None:
+        check_indices(inverse, -1, ref.shape[2], unique=False, what="pyramid_bwd inverse map")
     dev = ref.device
     outs = [torch.empty(B, S, H, D, dtype=torch.bfloat16, device=dev) if g is not None else None
             for g in (gq, gk, gv)]
@@ -408,6 +494,7 @@ def pyramid_rope_bwd(gq, gk, gv, inverse, freqs, B: int, S: int, H: int, L: int,
     """``pyramid_bwd`` with the rotary embedding's backward fused in: returns the
     gradient of the fused projection output, bf16 [B, S, 3*H*D] ([dq | dk | dv],
     dq and dk rotated back by -theta)."""
+    _need_rows("pyramid_rope_bwd grads", gq, gk, gv)
     _need_gpu(gq, gk, gv)
     _check_freqs(freqs, S, D)
     gb, gh, gs, _ = gq.stride()
@@ -508,13 +595,13 @@ def rmsnorm_bwd(dy, x, w, rstd, dres=None):
     """Grads of RMSNorm: ``(dx bf16 like x, dw bf16 like w)``; ``dres`` (optional) is
     added to dx (a residual branch's gradient)."""
     _need_gpu(dy, x, w, rstd)
-    dy = dy.contiguous()
+    dy, x, rstd = dy.contiguous(), x.contiguous(), rstd.contiguous()
     if dres is not None:
         dres = dres.contiguous()
     dim = x.shape[-1]
     rows = x.numel() // dim
-    dx = torch.empty_like(x)
-    dw = torch.empty_like(w)
+    dx = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    dw = torch.empty(w.shape, dtype=w.dtype, device=w.device)
     parts = min(RMSNORM_BWD_PARTS, rows)
     part = torch.empty(dim, parts, dtype=torch.float32, device=x.device)
     with torch.cuda.device(x.device):
@@ -539,10 +626,10 @@ def swiglu_fwd(h):
 
 def swiglu_bwd(da, h):
     _need_gpu(da, h)
-    da = da.contiguous()
+    da, h = da.contiguous(), h.contiguous()
     F2 = h.shape[-1]
     rows = h.numel() // F2
-    dh = torch.empty_like(h)
+    dh = torch.empty(h.shape, dtype=h.dtype, device=h.device)
     with torch.cuda.device(h.device):
         rc = lib().lh_swiglu_bwd(_ptr(da), _ptr(h), _ptr(dh), rows, F2 // 2, _stream(h.device))
     _check(rc, "lh_swiglu_bwd")

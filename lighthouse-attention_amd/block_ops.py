@@ -12,9 +12,14 @@ vendored with the reference; its wiring is ``lighthouse-attention.patch:583-769`
   that reads its result, in one pass each way.
 - ``swiglu``: ``F.silu(w1(x)) * w3(x)`` from one fused ``[h1 | h3]`` projection.
 
-There is no CPU path: every op raises without the GPU library.
+There is no CPU path: every op raises without the GPU library.  Under
+``torch.compile`` each op is a graph break (``torch.compiler.disable``), as the
+reference keeps its own native calls out of the graph; the Lighthouse layer
+itself is a traceable custom op.
 """
 from __future__ import annotations
+
+import functools
 
 import torch
 import torch.nn as nn
@@ -23,6 +28,20 @@ import torch.nn.functional as F
 from . import _native as N
 
 __all__ = ["linear", "rope_qkv", "rms_norm", "add_rms_norm", "swiglu", "RMSNorm", "wgrad_splits"]
+
+
+def graph_break(fn):
+    """Run ``fn`` as a graph break under ``torch.compile`` (``torch.compiler.disable``)
+    and as a plain call otherwise (no per-call wrapper cost in eager mode)."""
+    disabled = torch.compiler.disable(fn)
+
+    @functools.wraps(fn)
+    def wrapper(*args, **kwargs):
+        if torch.compiler.is_compiling():
+            return disabled(*args, **kwargs)
+        return fn(*args, **kwargs)
+
+    return wrapper
 
 
 def wgrad_splits(T: int, O: int, I: int, cus: int = 256) -> int:
@@ -75,6 +94,7 @@ def _need_bf16(*ts):
             raise TypeError(f"block ops compute in bfloat16; got {t.dtype}")
 
 
+@graph_break
 def linear(x, w):
     """``x @ w^T`` (bf16, no bias)."""
     _need_bf16(x, w)
@@ -103,6 +123,7 @@ class _RopeQKVFn(torch.autograd.Function):
         return N.rope_qkv_bwd(z(dq, Hq), z(dk, Hkv), z(dv, Hkv), freqs, Hq, Hkv, D), None, None, None, None
 
 
+@graph_break
 def rope_qkv(x, freqs, Hq: int, Hkv: int, D: int):
     """Fused projection output ``x`` [B, S, (Hq+2Hkv)*D] -> rotated q, rotated k, v,
     each [B, S, H, D] contiguous.  ``freqs``: fp32 [>=S, D/2, 2] (cos, sin), e.g.
@@ -114,6 +135,7 @@ def rope_qkv(x, freqs, Hq: int, Hkv: int, D: int):
 class _RMSNormFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w, eps):
+        x = x.contiguous()  # the backward reads the same rows the forward normalised
         y, rstd = N.rmsnorm_fwd(x, w, eps)
         ctx.save_for_backward(x, w, rstd)
         return y
@@ -125,6 +147,7 @@ class _RMSNormFn(torch.autograd.Function):
         return dx, dw, None
 
 
+@graph_break
 def rms_norm(x, w, eps: float):
     _need_bf16(x, w)
     return _RMSNormFn.apply(x, w, eps)
@@ -146,6 +169,7 @@ class _AddRMSNormFn(torch.autograd.Function):
         return dx, dx, dw, None
 
 
+@graph_break
 def add_rms_norm(x, r, w, eps: float):
     """``h = x + r`` and ``RMSNorm(h)`` in one pass: returns ``(h, y)``."""
     _need_bf16(x, r, w)
@@ -162,6 +186,7 @@ class RMSNorm(nn.RMSNorm):
 class _SwiGLUFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, h):
+        h = h.contiguous()
         ctx.save_for_backward(h)
         return N.swiglu_fwd(h)
 
@@ -171,6 +196,7 @@ class _SwiGLUFn(torch.autograd.Function):
         return N.swiglu_bwd(da, h)
 
 
+@graph_break
 def swiglu(h):
     """``[h1 | h3]`` (last dim 2F) -> ``silu(h1) * h3``."""
     _need_bf16(h)

@@ -389,3 +389,52 @@ extern "C" int lh_build_inverse(const int32_t* indices, int n, int32_t* inverse,
   }
   return LH_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Index validation (debug aid; the Python layer runs it in its check mode).
+// counts[0] += entries outside [lo, hi); with marks, counts[1] += entries whose
+// row was already named earlier by the same (b, h) (so counts[1] is the number
+// of duplicates: k copies of a row add k - 1).  Negative entries inside the
+// range (-1 with lo = -1: an empty slot) are not counted as duplicates.
+// ---------------------------------------------------------------------------
+__global__ void zero_counts_kernel(int32_t* __restrict__ counts) {
+  if (threadIdx.x < 2) counts[threadIdx.x] = 0;
+}
+
+__global__ void check_indices_kernel(const int32_t* __restrict__ idx, int n, int BH, int lo, int hi,
+                                     int32_t* __restrict__ marks, int32_t* __restrict__ counts) {
+  const size_t total = (size_t)BH * n;
+  int bad = 0, dup = 0;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const int r = idx[i];
+    if (r < lo || r >= hi) {
+      ++bad;
+    } else if (marks && r >= 0) {  // r == -1 (allowed when lo == -1) marks an empty slot
+      const size_t bh = i / n;
+      if (atomicAdd(&marks[bh * (size_t)(hi - lo) + (r - lo)], 1) != 0) ++dup;
+    }
+  }
+  if (bad) atomicAdd(&counts[0], bad);
+  if (dup) atomicAdd(&counts[1], dup);
+}
+
+extern "C" int lh_check_indices(const int32_t* indices, int B, int H, int n, int lo, int hi, int32_t* marks,
+                                int32_t* counts, void* stream) {
+  if (!indices || !counts || B <= 0 || H <= 0 || n < 0 || hi <= lo) return LH_ERR_INVALID_ARG;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(zero_counts_kernel, dim3(1), dim3(64), 0, st, counts);
+  LH_CHECK_LAUNCH();
+  if (marks) {
+    const size_t tot = (size_t)B * H * (size_t)(hi - lo);
+    const int blocks = (int)((tot + 255) / 256 < 65536 ? (tot + 255) / 256 : 65536);
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(blocks), dim3(256), 0, st, marks, tot, 0);
+    LH_CHECK_LAUNCH();
+  }
+  if (n > 0) {
+    const size_t tn = (size_t)B * H * n;
+    const int b2 = (int)((tn + 255) / 256 < 4096 ? (tn + 255) / 256 : 4096);
+    hipLaunchKernelGGL(check_indices_kernel, dim3(b2), dim3(256), 0, st, indices, n, B * H, lo, hi, marks, counts);
+    LH_CHECK_LAUNCH();
+  }
+  return LH_OK;
+}

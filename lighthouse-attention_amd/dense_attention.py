@@ -17,6 +17,7 @@ import torch
 import torch.nn as nn
 
 from . import _native as N
+from .block_ops import graph_break
 from .lighthouse_selection import _mark
 
 __all__ = ["dense_causal_attention", "ScaledDotProductAttention"]
@@ -53,6 +54,7 @@ class _DenseCausalFn(torch.autograd.Function):
         return dq, dk, dv
 
 
+@graph_break
 def dense_causal_attention(q, k, v):
     """Causal softmax attention, scale 1/sqrt(D): ``q, k, v`` bf16 ``[B, H, S, D]``
     (any batch/head/seq strides, D contiguous) -> ``[B, H, S, D]``."""

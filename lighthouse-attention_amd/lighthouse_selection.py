@@ -93,7 +93,7 @@ def _base_rows(xq, xk, xv, pq=None, pk=None, pv=None):
     if pq is None:
         return N.Rows(xq, xk, xv, (sb, ss, sh))
     pb, ps, ph, _ = pq.stride()
-    return N.Rows(xq, xk, xv, (sb, ss, sh), pq, pk, pv, (pb, ps, ph), split=S)
+    return N.Rows(xq, xk, xv, (sb, ss, sh), pq, pk, pv, (pb, ps, ph), split=S, limit=S + pq.shape[1])
 
 
 _op_hook = None
@@ -116,57 +116,74 @@ def _mark(name):
         _op_hook(name)
 
 
-class _LighthouseLayerFn(torch.autograd.Function):
-    """Whole layer: pyramid -> selection -> gathered causal attention -> fan-out.
+def _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major):
+    """Forward of the whole layer on contiguous bf16 [B, S, H, D] inputs:
+    pyramid -> selection -> gathered causal attention -> fan-out.  Returns
+    ``(out, idx, saved)`` with ``saved = (pq, pk, pv, inv, o, lse)``."""
+    B, S, H, D = xq.shape
+    _, _, S_tot = N.pyramid_lengths(S, L, p)
+    _, _, _, S_sel = N.geometry(S, L, p, topk, strict)
+    _mark("fwd_start")
+    if dilation:
+        scores = N.dilated_scores(xq, xk, xv, dilation, S_tot)
+        _mark("dilated_scores")
+        pq, pk, pv, sqk, skq = N.pyramid_fwd(xq, xk, xv, L, p, scores=scores)
+    else:
+        pq, pk, pv, sqk, skq = N.pyramid_fwd(xq, xk, xv, L, p)
+    _mark("pyramid")
+    idx, inv = N.select_topk(sqk, skq, S, L, p, topk, tie=tie, strict=strict)
+    _mark("select")
+    rows = _base_rows(xq, xk, xv, pq, pk, pv)
+    o, lse = N.attn_fwd(rows, idx, B, H, S_sel, D)
+    _mark("attn_fwd")
+    out = N.scatter_fwd(o, inv, S, S, L, p, seq_major=seq_major)
+    _mark("scatter_fwd")
+    return out, idx, (pq, pk, pv, inv, o, lse)
 
-    Backward: fan-out adjoint (+ softmax delta) -> attention backward in
-    selected space -> pyramid backward onto the base rows.
-    """
+
+def _attn_bwd_pair(rows, idx, B, H, S_sel, dattn, lse, delta, D):
+    dks, dvs = N.attn_bwd_dkdv(rows, idx, B, H, S_sel, dattn, lse, delta, D)
+    _mark("attn_bwd_dkdv")
+    dqs = N.attn_bwd_dq(rows, idx, B, H, S_sel, dattn, lse, delta, D)
+    _mark("attn_bwd_dq")
+    return dqs, dks, dvs
+
+
+def _layer_bwd(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, L, p):
+    """Backward of ``_layer_fwd``: fan-out adjoint (+ softmax delta) -> attention
+    backward in selected space -> pyramid backward onto the base rows."""
+    B, S, H, D = xq.shape
+    S_sel = idx.shape[-1]
+    _mark("bwd_start")
+    dattn, delta = N.scatter_bwd(dout, idx, o, S, L, p)
+    _mark("scatter_bwd")
+    rows = _base_rows(xq, xk, xv, pq, pk, pv)
+    dqs, dks, dvs = _attn_bwd_pair(rows, idx, B, H, S_sel, dattn, lse, delta, D)
+    dxq, dxk, dxv = N.pyramid_bwd(dqs, dks, dvs, inv, B, S, H, L, p, D)
+    _mark("pyramid_bwd")
+    return dxq, dxk, dxv
+
+
+class _LighthouseLayerFn(torch.autograd.Function):
+    """Whole layer (``_layer_fwd`` / ``_layer_bwd``) as one autograd node."""
 
     @staticmethod
     def forward(ctx, xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major):
-        B, S, H, D = xq.shape
         xq, xk, xv = xq.contiguous(), xk.contiguous(), xv.contiguous()
-        lens, offs, S_tot = N.pyramid_lengths(S, L, p)
-        _, _, _, S_sel = N.geometry(S, L, p, topk, strict)
-        _mark("fwd_start")
-        if dilation:
-            scores = N.dilated_scores(xq, xk, xv, dilation, S_tot)
-            _mark("dilated_scores")
-            pq, pk, pv, sqk, skq = N.pyramid_fwd(xq, xk, xv, L, p, scores=scores)
-        else:
-            pq, pk, pv, sqk, skq = N.pyramid_fwd(xq, xk, xv, L, p)
-        _mark("pyramid")
-        idx, inv = N.select_topk(sqk, skq, S, L, p, topk, tie=tie, strict=strict)
-        _mark("select")
-        rows = _base_rows(xq, xk, xv, pq, pk, pv)
-        o, lse = N.attn_fwd(rows, idx, B, H, S_sel, D)
-        _mark("attn_fwd")
-        out = N.scatter_fwd(o, inv, S, S, L, p, seq_major=seq_major)
-        _mark("scatter_fwd")
+        out, idx, (pq, pk, pv, inv, o, lse) = _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation,
+                                                         seq_major)
         ctx.save_for_backward(xq, xk, xv, pq, pk, pv, idx, inv, o, lse)
-        ctx.geo = (B, S, H, D, L, p, S_sel)
+        ctx.geo = (L, p)
         ctx.mark_non_differentiable(idx)
         ctx.set_materialize_grads(False)  # no zero-filled gradient for the index output
         return out, idx
 
     @staticmethod
     def backward(ctx, dout, _didx):
-        xq, xk, xv, pq, pk, pv, idx, inv, o, lse = ctx.saved_tensors
-        B, S, H, D, L, p, S_sel = ctx.geo
         if dout is None:
-            return None, None, None, None, None, None, None, None, None, None
-        _mark("bwd_start")
-        dattn, delta = N.scatter_bwd(dout, idx, o, S, L, p)
-        _mark("scatter_bwd")
-        rows = _base_rows(xq, xk, xv, pq, pk, pv)
-        dks, dvs = N.attn_bwd_dkdv(rows, idx, B, H, S_sel, dattn, lse, delta, D)
-        _mark("attn_bwd_dkdv")
-        dqs = N.attn_bwd_dq(rows, idx, B, H, S_sel, dattn, lse, delta, D)
-        _mark("attn_bwd_dq")
-        dxq, dxk, dxv = N.pyramid_bwd(dqs, dks, dvs, inv, B, S, H, L, p, D)
-        _mark("pyramid_bwd")
-        return dxq, dxk, dxv, None, None, None, None, None, None, None
+            return (None,) * 10
+        dx = _layer_bwd(dout, *ctx.saved_tensors, *ctx.geo)
+        return dx + (None,) * 7
 
 
 def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, topk: int = 1024,
@@ -176,7 +193,9 @@ def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, t
 
     ``dilation > 0`` selects the dilated scorer, 0 the norm scorer.  ``seq_major``
     stores ``out`` as ``[B, S, H, D]`` (the returned tensor is its ``[B, H, S, D]``
-    view), which is the layout the model's output projection reads."""
+    view), which is the layout the model's output projection reads.  Under
+    ``torch.compile`` the layer is one registered custom op (traced without a
+    graph break); eagerly it is an ``autograd.Function``; both run the same kernels."""
     if xq.shape[-1] != N.D_SUPPORTED:
         raise ValueError(f"head_dim must be {N.D_SUPPORTED}, got {xq.shape[-1]}")
     if not (xq.shape == xk.shape == xv.shape):
@@ -184,8 +203,47 @@ def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, t
     for t in (xq, xk, xv):
         if t.dtype != torch.bfloat16:
             raise TypeError("the native layer computes in bfloat16; got " + str(t.dtype))
+    if tie_break not in N.TIE_MODES:
+        raise ValueError(f"tie_break must be one of {sorted(N.TIE_MODES)}, got {tie_break!r}")
+    if torch.compiler.is_compiling():
+        out, idx = _compiled_ops.layer_fwd(xq, xk, xv, num_levels, pooling_factor, topk, tie_break, bool(strict),
+                                           int(dilation), bool(seq_major))[:2]
+        return out, idx
     return _LighthouseLayerFn.apply(xq, xk, xv, num_levels, pooling_factor, topk, tie_break, strict,
                                     int(dilation), bool(seq_major))
+
+
+def _rope_layer_fwd(xqkv, freqs, H, L, p, topk, tie, strict, seq_major):
+    """Forward of the layer fed from the fused [q | k | v] projection output; returns
+    ``(out, idx, saved)`` with ``saved = (xr, pq, pk, pv, inv, o, lse)``."""
+    B, S, W = xqkv.shape
+    D = W // (3 * H)
+    _, _, _, S_sel = N.geometry(S, L, p, topk, strict)
+    _mark("fwd_start")
+    xr, pq, pk, pv, sqk, skq = N.rope_pyramid_fwd(xqkv, freqs, H, L, p, D)
+    _mark("pyramid")
+    idx, inv = N.select_topk(sqk, skq, S, L, p, topk, tie=tie, strict=strict)
+    _mark("select")
+    rows = _rope_rows(xqkv, xr, H, D, pq, pk, pv)
+    o, lse = N.attn_fwd(rows, idx, B, H, S_sel, D)
+    _mark("attn_fwd")
+    out = N.scatter_fwd(o, inv, S, S, L, p, seq_major=seq_major)
+    _mark("scatter_fwd")
+    return out, idx, (xr, pq, pk, pv, inv, o, lse)
+
+
+def _rope_layer_bwd(dout, xqkv, freqs, xr, pq, pk, pv, idx, inv, o, lse, H, L, p):
+    B, S, W = xqkv.shape
+    D = W // (3 * H)
+    S_sel = idx.shape[-1]
+    _mark("bwd_start")
+    dattn, delta = N.scatter_bwd(dout, idx, o, S, L, p)
+    _mark("scatter_bwd")
+    rows = _rope_rows(xqkv, xr, H, D, pq, pk, pv)
+    dqs, dks, dvs = _attn_bwd_pair(rows, idx, B, H, S_sel, dattn, lse, delta, D)
+    dx = N.pyramid_rope_bwd(dqs, dks, dvs, inv, freqs, B, S, H, L, p, D)
+    _mark("pyramid_bwd")
+    return dx
 
 
 class _LighthouseRopeLayerFn(torch.autograd.Function):
@@ -197,42 +255,20 @@ class _LighthouseRopeLayerFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, xqkv, freqs, H, L, p, topk, tie, strict, seq_major):
-        B, S, W = xqkv.shape
-        D = W // (3 * H)
-        _, _, _, S_sel = N.geometry(S, L, p, topk, strict)
-        _mark("fwd_start")
-        xr, pq, pk, pv, sqk, skq = N.rope_pyramid_fwd(xqkv, freqs, H, L, p, D)
-        _mark("pyramid")
-        idx, inv = N.select_topk(sqk, skq, S, L, p, topk, tie=tie, strict=strict)
-        _mark("select")
-        rows = _rope_rows(xqkv, xr, H, D, pq, pk, pv)
-        o, lse = N.attn_fwd(rows, idx, B, H, S_sel, D)
-        _mark("attn_fwd")
-        out = N.scatter_fwd(o, inv, S, S, L, p, seq_major=seq_major)
-        _mark("scatter_fwd")
-        ctx.save_for_backward(xqkv, xr, freqs, pq, pk, pv, idx, inv, o, lse)
-        ctx.geo = (B, S, H, D, L, p, S_sel)
+        out, idx, saved = _rope_layer_fwd(xqkv, freqs, H, L, p, topk, tie, strict, seq_major)
+        xr, pq, pk, pv, inv, o, lse = saved
+        ctx.save_for_backward(xqkv, freqs, xr, pq, pk, pv, idx, inv, o, lse)
+        ctx.geo = (H, L, p)
         ctx.mark_non_differentiable(idx)
         ctx.set_materialize_grads(False)
         return out, idx
 
     @staticmethod
     def backward(ctx, dout, _didx):
-        xqkv, xr, freqs, pq, pk, pv, idx, inv, o, lse = ctx.saved_tensors
-        B, S, H, D, L, p, S_sel = ctx.geo
         if dout is None:
             return (None,) * 9
-        _mark("bwd_start")
-        dattn, delta = N.scatter_bwd(dout, idx, o, S, L, p)
-        _mark("scatter_bwd")
-        rows = _rope_rows(xqkv, xr, H, D, pq, pk, pv)
-        dks, dvs = N.attn_bwd_dkdv(rows, idx, B, H, S_sel, dattn, lse, delta, D)
-        _mark("attn_bwd_dkdv")
-        dqs = N.attn_bwd_dq(rows, idx, B, H, S_sel, dattn, lse, delta, D)
-        _mark("attn_bwd_dq")
-        dx = N.pyramid_rope_bwd(dqs, dks, dvs, inv, freqs, B, S, H, L, p, D)
-        _mark("pyramid_bwd")
-        return dx, None, None, None, None, None, None, None, None
+        dx = _rope_layer_bwd(dout, *ctx.saved_tensors, *ctx.geo)
+        return (dx,) + (None,) * 8
 
 
 def _rope_rows(xqkv, xr, H, D, pq, pk, pv):
@@ -242,7 +278,7 @@ def _rope_rows(xqkv, xr, H, D, pq, pk, pv):
     v = xqkv[..., 2 * hd:]
     sb, ss, _ = xqkv.stride()
     pb, ps, ph, _ = pq.stride()
-    return N.Rows(q, k, v, (sb, ss, D), pq, pk, pv, (pb, ps, ph), split=S)
+    return N.Rows(q, k, v, (sb, ss, D), pq, pk, pv, (pb, ps, ph), split=S, limit=S + pq.shape[1])
 
 
 def lighthouse_layer_rope(xqkv, freqs, n_heads: int, num_levels: int = 3, pooling_factor: int = 4,
@@ -261,11 +297,125 @@ def lighthouse_layer_rope(xqkv, freqs, n_heads: int, num_levels: int = 3, poolin
         raise ValueError(f"xqkv must hold 3 x {n_heads} heads of dim {N.D_SUPPORTED}, got width {W}")
     if xqkv.dtype != torch.bfloat16:
         raise TypeError("the native layer computes in bfloat16; got " + str(xqkv.dtype))
+    if tie_break not in N.TIE_MODES:
+        raise ValueError(f"tie_break must be one of {sorted(N.TIE_MODES)}, got {tie_break!r}")
     if xqkv.stride(2) != 1 or xqkv.stride(1) % 8 or xqkv.stride(0) != S * xqkv.stride(1):
         xqkv = xqkv.contiguous()
     freqs = freqs.contiguous()
+    if torch.compiler.is_compiling():
+        out, idx = _compiled_ops.rope_layer_fwd(xqkv, freqs, n_heads, num_levels, pooling_factor, topk, tie_break,
+                                                bool(strict), bool(seq_major))[:2]
+        return out, idx
     return _LighthouseRopeLayerFn.apply(xqkv, freqs, n_heads, num_levels, pooling_factor, topk, tie_break, strict,
                                         bool(seq_major))
+
+
+class _CompiledOps:
+    """The two layer forms as ``torch.library`` custom ops with fake (meta)
+    implementations and registered autograd, so ``torch.compile`` traces a
+    caller's block through the layer without a graph break.  The reference marks
+    its selection ``@torch.compiler.disable`` and compiles each block with
+    ``fullgraph=False`` (``lighthouse-attention.patch:9-12,540-548``).  Saved
+    tensors are extra outputs of the forward op (custom ops cannot hold state);
+    the backward is a second op."""
+
+    def __init__(self):
+        lib = "lighthouse_amd"
+        if hasattr(torch.ops, lib) and hasattr(getattr(torch.ops, lib), "layer_fwd"):
+            ops = getattr(torch.ops, lib)  # already registered by an earlier import of this module
+            self.layer_fwd, self.rope_layer_fwd = ops.layer_fwd, ops.rope_layer_fwd
+            return
+
+        @torch.library.custom_op(f"{lib}::layer_fwd", mutates_args=(), schema=(
+            "(Tensor xq, Tensor xk, Tensor xv, int L, int p, int topk, str tie, bool strict, int dilation, "
+            "bool seq_major) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)"))
+        def layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major):
+            xq, xk, xv = xq.contiguous(), xk.contiguous(), xv.contiguous()
+            out, idx, saved = _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major)
+            return (out, idx) + saved
+
+        @layer_fwd.register_fake
+        def _(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major):
+            B, S, H, D = xq.shape
+            _, _, S_tot = N.pyramid_lengths(S, L, p)
+            S_sel = N.geometry(S, L, p, topk, strict)[3]
+            out = xq.new_empty(B, S, H, D).transpose(1, 2) if seq_major else xq.new_empty(B, H, S, D)
+            pooled = [xq.new_empty(B, S_tot - S, H, D) for _ in range(3)]
+            return (out, xq.new_empty(B, H, S_sel, dtype=torch.int32), *pooled,
+                    xq.new_empty(B, H, S_tot, dtype=torch.int32), xq.new_empty(B, H, S_sel, D),
+                    xq.new_empty(B, H, S_sel, dtype=torch.float32))
+
+        @torch.library.custom_op(f"{lib}::layer_bwd", mutates_args=(), schema=(
+            "(Tensor dout, Tensor xq, Tensor xk, Tensor xv, Tensor pq, Tensor pk, Tensor pv, Tensor idx, "
+            "Tensor inv, Tensor o, Tensor lse, int L, int p) -> (Tensor, Tensor, Tensor)"))
+        def layer_bwd(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, L, p):
+            xq, xk, xv = xq.contiguous(), xk.contiguous(), xv.contiguous()
+            return _layer_bwd(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, L, p)
+
+        @layer_bwd.register_fake
+        def _(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, L, p):
+            return tuple(torch.empty(xq.shape, dtype=xq.dtype, device=xq.device) for _ in range(3))
+
+        def layer_setup(ctx, inputs, output):
+            xq, xk, xv, L, p = inputs[:5]
+            ctx.save_for_backward(xq, xk, xv, *output[2:5], output[1], *output[5:])
+            ctx.geo = (L, p)
+
+        def layer_grad(ctx, dout, *_unused):
+            if dout is None:
+                return (None,) * 10
+            xq, xk, xv, pq, pk, pv, idx, inv, o, lse = ctx.saved_tensors
+            dx = layer_bwd(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, *ctx.geo)
+            return tuple(dx) + (None,) * 7
+
+        layer_fwd.register_autograd(layer_grad, setup_context=layer_setup)
+
+        @torch.library.custom_op(f"{lib}::rope_layer_fwd", mutates_args=(), schema=(
+            "(Tensor xqkv, Tensor freqs, int H, int L, int p, int topk, str tie, bool strict, bool seq_major) -> "
+            "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)"))
+        def rope_layer_fwd(xqkv, freqs, H, L, p, topk, tie, strict, seq_major):
+            out, idx, saved = _rope_layer_fwd(xqkv, freqs, H, L, p, topk, tie, strict, seq_major)
+            return (out, idx) + saved
+
+        @rope_layer_fwd.register_fake
+        def _(xqkv, freqs, H, L, p, topk, tie, strict, seq_major):
+            B, S, W = xqkv.shape
+            D = W // (3 * H)
+            _, _, S_tot = N.pyramid_lengths(S, L, p)
+            S_sel = N.geometry(S, L, p, topk, strict)[3]
+            e = xqkv.new_empty
+            out = e(B, S, H, D).transpose(1, 2) if seq_major else e(B, H, S, D)
+            xr = xqkv.new_empty_strided(xqkv.shape, xqkv.stride())
+            pooled = [e(B, S_tot - S, H, D) for _ in range(3)]
+            return (out, e(B, H, S_sel, dtype=torch.int32), xr, *pooled, e(B, H, S_tot, dtype=torch.int32),
+                    e(B, H, S_sel, D), e(B, H, S_sel, dtype=torch.float32))
+
+        @torch.library.custom_op(f"{lib}::rope_layer_bwd", mutates_args=(), schema=(
+            "(Tensor dout, Tensor xqkv, Tensor freqs, Tensor xr, Tensor pq, Tensor pk, Tensor pv, Tensor idx, "
+            "Tensor inv, Tensor o, Tensor lse, int H, int L, int p) -> Tensor"))
+        def rope_layer_bwd(dout, xqkv, freqs, xr, pq, pk, pv, idx, inv, o, lse, H, L, p):
+            return _rope_layer_bwd(dout, xqkv, freqs, xr, pq, pk, pv, idx, inv, o, lse, H, L, p)
+
+        @rope_layer_bwd.register_fake
+        def _(dout, xqkv, freqs, xr, pq, pk, pv, idx, inv, o, lse, H, L, p):
+            return torch.empty(xqkv.shape, dtype=xqkv.dtype, device=xqkv.device)
+
+        def rope_setup(ctx, inputs, output):
+            xqkv, freqs, H, L, p = inputs[:5]
+            ctx.save_for_backward(xqkv, freqs, *output[2:6], output[1], *output[6:])
+            ctx.geo = (H, L, p)
+
+        def rope_grad(ctx, dout, *_unused):
+            if dout is None:
+                return (None,) * 9
+            dx = rope_layer_bwd(dout, *ctx.saved_tensors, *ctx.geo)
+            return (dx,) + (None,) * 8
+
+        rope_layer_fwd.register_autograd(rope_grad, setup_context=rope_setup)
+        self.layer_fwd, self.rope_layer_fwd = layer_fwd, rope_layer_fwd
+
+
+_compiled_ops = _CompiledOps()
 
 
 class _PyramidCatFn(torch.autograd.Function):
@@ -315,7 +465,8 @@ class _GatheredAttnFn(torch.autograd.Function):
         assert k_cat.stride() == q_cat.stride() == v_cat.stride(), "scorer outputs must share strides"
         sb, sh, ss, _ = q_cat.stride()
         st = (sb, ss, sh)
-        return N.Rows(q_cat, k_cat, v_cat, st, q_cat, k_cat, v_cat, st, split=q_cat.shape[2])
+        return N.Rows(q_cat, k_cat, v_cat, st, q_cat, k_cat, v_cat, st, split=q_cat.shape[2],
+                      limit=q_cat.shape[2])
 
     @staticmethod
     def forward(ctx, q_cat, k_cat, v_cat, idx):
@@ -345,9 +496,13 @@ class _ScatterToBaseFn(torch.autograd.Function):
     """``_ScatterToBaseAutograd`` (``src/lighthouse_selection.py:517-576``), gather-formulated."""
 
     @staticmethod
-    def forward(ctx, attn_out, indices, N_shard, N_total, num_levels, pooling_factor):
+    def forward(ctx, attn_out, indices, N_shard, N_total, num_levels, pooling_factor, validate):
         _, _, S_tot = N.pyramid_lengths(N_shard, num_levels, pooling_factor)
         idx = indices.to(torch.int32).contiguous()
+        if validate:
+            # the gather formulation needs each row named at most once per (b, h); -1 marks an
+            # empty slot (skipped, as the reference's kernels skip it)
+            N.check_indices(idx, -1, S_tot, unique=True, what="scatter_to_base_sequence indices")
         inv = N.build_inverse(idx, S_tot)
         out = N.scatter_fwd(attn_out, inv, N_shard, N_total, num_levels, pooling_factor)
         ctx.save_for_backward(idx)
@@ -359,19 +514,26 @@ class _ScatterToBaseFn(torch.autograd.Function):
         (idx,) = ctx.saved_tensors
         S, L, p = ctx.geo
         dattn, _ = N.scatter_bwd(grad_output, idx, None, S, L, p)
-        return dattn, None, None, None, None, None
+        return dattn, None, None, None, None, None, None
 
 
 def scatter_to_base_sequence(attn_out, indices_hp, rank_ids_hp, N_shard: int, N_total: int,
-                             num_levels: int, pooling_factor: int):
+                             num_levels: int, pooling_factor: int, validate: bool = True):
     """Fan-out of selected rows onto the base sequence (``src/lighthouse_selection.py:758-770``).
 
     Only the single-shard form is built: ``rank_ids_hp`` must be all zeros,
-    which is what every reference caller passes (:817, :1045-1046)."""
+    which is what every reference caller passes (:817, :1045-1046).
+    ``attn_out`` must be bfloat16 (``TypeError`` otherwise).  The fan-out is
+    gather-formulated, so every (b, h) must name each pyramid row at most once;
+    ``validate`` (default) checks that and the index range on the device and
+    raises ``IndexError`` (one stream synchronisation); entries of -1 are empty
+    slots, skipped as in the reference."""
     if rank_ids_hp is not None and bool((rank_ids_hp != 0).any()):
         raise NotImplementedError("non-zero rank_ids (sharded fan-out) belong to the context-parallel path, "
                                   "which this single-GPU build does not include")
-    return _ScatterToBaseFn.apply(attn_out, indices_hp, N_shard, N_total, num_levels, pooling_factor)
+    N._need_rows("scatter_to_base_sequence attn_out", attn_out)
+    return _ScatterToBaseFn.apply(attn_out, indices_hp, N_shard, N_total, num_levels, pooling_factor,
+                                  bool(validate))
 
 
 # ---------------------------------------------------------------------------
@@ -512,7 +674,9 @@ class LighthouseLocal(nn.Module):
             gi = idx.long().unsqueeze(-1).expand(-1, -1, -1, d)
             attn_out = self.attention(torch.gather(xq_cat, 2, gi), torch.gather(xk_cat, 2, gi),
                                       torch.gather(xv_cat, 2, gi))
-        return scatter_to_base_sequence(attn_out, idx, None, s, s, self.num_levels, self.pooling_factor)
+        # indices from this module's selection are unique and in range by construction
+        return scatter_to_base_sequence(attn_out, idx, None, s, s, self.num_levels, self.pooling_factor,
+                                        validate=False)
 
 
 class DialatedLighthouseNormScorerCP(nn.Module):

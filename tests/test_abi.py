@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol(pkg):
     for n in _declared():
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
     assert set(_declared()) == set(pkg._native.EXPORTED)
-    assert lib.lh_abi_version() == 3
+    assert lib.lh_abi_version() == 4
 
 
 def test_strerror(pkg):
@@ -151,3 +151,33 @@ def test_selection_class_asserts_like_reference(pkg):
         pkg.LighthouseSelectionQkKqChunkedTopkNvrtc.forward(s, s, 3, 4, 256, 4096)
     with pytest.raises(AssertionError):
         pkg.LighthouseSelectionQkKqChunkedTopkNvrtc.forward(s, s[..., :10], 3, 4, 256, 4096)
+
+
+def test_check_indices_host_validation(pkg):
+    lib = pkg._native.lib()
+    null = ctypes.c_void_p(0)
+    assert lib.lh_check_indices(null, 1, 1, 8, 0, 10, null, null, null) == 1
+    assert lib.lh_check_indices(ctypes.c_void_p(16), 1, 1, 8, 5, 5, null, ctypes.c_void_p(16), null) == 1
+
+
+def test_row_kernels_refuse_non_bf16(pkg):
+    """The kernels read and write bf16 rows: other dtypes raise TypeError on the
+    host before any device work (CPU tensors suffice to reach the check)."""
+    N = pkg._native
+    x32 = torch.zeros(1, 2, 16, 128)
+    idx = torch.zeros(1, 2, 16, dtype=torch.int32)
+    with pytest.raises(TypeError):
+        N.scatter_fwd(x32, idx, 16, 16, 2, 2)
+    with pytest.raises(TypeError):
+        N.scatter_bwd(x32, idx, None, 16, 2, 2)
+    with pytest.raises(TypeError):
+        N.Rows(x32, x32, x32, (0, 0, 0))
+    with pytest.raises(TypeError):
+        N.pyramid_bwd(x32, x32, x32, None, 1, 16, 2, 2, 2)
+    with pytest.raises(TypeError):
+        pkg.scatter_to_base_sequence(x32, idx, None, 16, 16, 2, 2)
+    xb = torch.zeros(1, 2, 16, 128, dtype=torch.bfloat16)
+    with pytest.raises(TypeError):  # int64 indices where the kernels read int32
+        N.attn_fwd(N.Rows(xb, xb, xb, (0, 0, 0)), idx.long(), 1, 2, 16)
+    with pytest.raises(ValueError):  # head dimension not contiguous
+        N.Rows(xb.transpose(-1, -2), xb, xb, (0, 0, 0))

@@ -30,6 +30,7 @@ CASES = [  # (workload, heads checked against the fp32 oracle)
     ("cfg3_k3072", (6,)),
     ("cfg3_k6144", (1,)),
     ("cfg4", (2,)),
+    ("cfg5_layer", (4,)),
 ]
 
 

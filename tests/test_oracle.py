@@ -405,3 +405,56 @@ def test_golden_selection(name):
         got = O.select_indices(g["scores_qk"], g["scores_kq"], L, p, k, S, tie=tie, strict=meta["strict"])
         assert np.array_equal(got, g[f"indices_{tie}"])
         assert hashlib.sha256(got.tobytes()).hexdigest() == meta[f"sha256_{tie}"]
+
+
+# ----------------------------------------------------------------------------- sanitizer build
+SAN_GEOS = [  # (S, L, p, k, strict)
+    (2048, 3, 4, 128, True),
+    (8192, 4, 2, 256, True),
+    (4096, 3, 4, 1536, False),   # cfg1 geometry (NCC < 128)
+    (5000, 3, 4, 256, False),    # S not a multiple of p^(L-1)
+    (16384, 5, 2, 256, False),
+]
+
+
+@pytest.fixture(scope="module")
+def asan_driver():
+    import shutil
+    import subprocess
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    subprocess.run(["make", "-s", "-C", os.path.join(O.__file__.rsplit(os.sep, 1)[0]), "asan"], check=True)
+    path = os.path.join(os.path.dirname(O.__file__), "_build", "select_ref_asan")
+    libs = subprocess.run(["ldd", path], capture_output=True, text=True).stdout
+    assert "libasan" in libs and "libubsan" in libs, "driver is not built with the sanitizers"
+    return path
+
+
+@pytest.mark.parametrize("tie", ["reference", "lower_index"])
+@pytest.mark.parametrize("geo", SAN_GEOS)
+def test_select_ref_under_sanitizers(asan_driver, tmp_path, geo, tie):
+    """oracle/select_ref.c run under AddressSanitizer + UBSan (any out-of-bounds
+    slot write, overflow or invalid shift aborts the driver), on strict and
+    generalized geometries with tie-heavy scores; the result equals the
+    regular build's."""
+    import subprocess
+    S, L, p, k, strict = geo
+    H = 2
+    S_tot = sum(O.level_lengths(S, L, p))
+    g = torch.Generator().manual_seed(S + L)
+    a = ((torch.randn(1, H, S_tot, generator=g).abs() * 4 + 8).bfloat16().float()).numpy()
+    b = ((torch.randn(1, H, S_tot, generator=g).abs() * 4 + 8).bfloat16().float()).numpy()
+    n = O.tile_geometry(S, L, p, k).S_sel
+    expect = R.select_indices_c(a, b, L, p, k, S, n, tie=tie, strict=strict)
+    fa, fb, fo = tmp_path / "qk.f32", tmp_path / "kq.f32", tmp_path / "out.i32"
+    a.astype(np.float32).tofile(fa)
+    b.astype(np.float32).tofile(fb)
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0:verify_asan_link_order=0",
+               UBSAN_OPTIONS="print_stacktrace=1")
+    r = subprocess.run([asan_driver, str(H), str(S_tot), str(S), str(L), str(p), str(k),
+                        str(int(tie == "lower_index")), "0" if strict else "1", str(n), str(fa), str(fb), str(fo)],
+                       capture_output=True, text=True, env=env, timeout=120)
+    assert r.returncode == 0, f"sanitized driver failed ({r.returncode}): {r.stderr[-2000:]}"
+    assert "runtime error" not in r.stderr and "AddressSanitizer" not in r.stderr, r.stderr[-2000:]
+    got = np.fromfile(fo, dtype=np.int32).reshape(1, H, n)
+    assert np.array_equal(got, expect)
