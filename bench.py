@@ -205,12 +205,32 @@ def op_stats(marks, work):
     return kernels
 
 
+def profiled_counters(workload, kernel):
+    """Matrix-core busy share and effective clock of `kernel` from the committed
+    rocprofv3 counter summary (SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE), or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "mfma_counters.json")) as f:
+            return json.load(f)["per_kernel"].get(workload, {}).get(kernel)
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def roofline_of(kernels, dom, workload):
     kd = kernels[dom]
     mfma = kd["unit"] == "TFLOP/s"
-    return {"kernel": dom, "bound": "mfma" if mfma else "hbm", "achieved": kd["achieved"],
-            "peak": BF16_PEAK_TFLOPS if mfma else HBM_PEAK_GBS, "unit": kd["unit"], "frac": kd["frac"],
-            "traffic": measured_traffic(workload, dom)}
+    r = {"kernel": dom, "bound": "mfma" if mfma else "hbm", "achieved": kd["achieved"],
+         "peak": BF16_PEAK_TFLOPS if mfma else HBM_PEAK_GBS, "unit": kd["unit"], "frac": kd["frac"],
+         "traffic": measured_traffic(workload, dom)}
+    if r["traffic"] is not None:
+        r["traffic_source"] = ("profiles/hbm_traffic.json: rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1 per launch "
+                               "(copy-calibrated) of an earlier run of this command, not measured in this run")
+    c = profiled_counters(workload, dom) if mfma else None
+    if c is not None:
+        r["mfma_busy_pct_profiled"] = c["mfma_busy_pct"]
+        r["clock_ghz_profiled"] = c["clock_ghz"]
+        r["counters_source"] = ("profiles/mfma_counters.json: rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES / "
+                                "(GRBM_GUI_ACTIVE per XCD x 1024 SIMDs) of an earlier run of this command")
+    return r
 
 
 def run_model(args, pkg, torch):
