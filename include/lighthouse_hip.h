@@ -308,6 +308,19 @@ int lh_rmsnorm_bwd(const void *dy, const void *x, const void *w, const float *rs
                    void *dx, void *dw, float *dw_part, int parts, int64_t rows, int dim, void *stream);
 
 /*
+ * lh_rmsnorm_bwd without the dw_part workspace: the per-block dw partials live in
+ * a static device array of the library (256 partials x 4096 columns fp32 = 4 MiB per
+ * GPU, held until the process ends), so this entry point allocates nothing and
+ * takes no workspace.  No counterpart in the reference; it is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same results as lh_rmsnorm_bwd with parts = 256.
+ * dim <= 4096 (LH_ERR_UNSUPPORTED otherwise).  All calls on one GPU share the
+ * array: calls that overlap on one GPU (other streams, other threads) race.
+ */
+int lh_rmsnorm_bwd_noalloc(const void *dy, const void *x, const void *w, const float *rstd, const void *dres,
+                           void *dx, void *dw, int64_t rows, int dim, void *stream);
+
+/*
  * SwiGLU on the fused [h1 | h3] projection (rows of 2F): a = bf16(bf16(silu(h1)) h3).
  * Replaces F.silu(w1(x)) * w3(x) of FeedForward (torchtitan llama3 model).
  */

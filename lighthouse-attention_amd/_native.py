@@ -62,6 +62,7 @@ _SIGS = {
     "lh_rmsnorm_fwd": (_I, [_P, _P, _P, _P, _L, _I, _F, _P]),
     "lh_add_rmsnorm_fwd": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _F, _P]),
     "lh_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _P]),
+    "lh_rmsnorm_bwd_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _L, _I, _P]),
     "lh_swiglu_fwd": (_I, [_P, _P, _L, _I, _P]),
     "lh_swiglu_bwd": (_I, [_P, _P, _P, _L, _I, _P]),
     "lh_splitk_sum": (_I, [_P, _P, _I, _L, _P]),

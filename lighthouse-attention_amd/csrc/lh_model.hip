@@ -5,6 +5,8 @@
 // row read once; fp32 arithmetic, one rounding to bf16 per output.
 #include "lh_common.h"
 
+#include <mutex>
+
 namespace {
 
 constexpr int kVec = 8;  // bf16 per 16-byte access
@@ -391,6 +393,48 @@ extern "C" int lh_rmsnorm_bwd(const void* dy, const void* x, const void* w, cons
   rmsnorm_dw_kernel<<<(dim + 3) / 4, 256, 0, (hipStream_t)stream>>>(dw_part, (bf16_t*)dw, used, dim);
   LH_CHECK_LAUNCH();
   return LH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm backward without a caller workspace: the dw partials live in a
+// file-scope device array (one copy per GPU, held until the process ends).
+// Its device address is looked up once per device with hipGetSymbolAddress;
+// in host code the array's name is only a host-side stand-in.  Every launch
+// writes each partial it later reads, so nothing needs clearing.  Calls that
+// overlap on one GPU share the array and race.
+// ---------------------------------------------------------------------------
+constexpr int kNoAllocParts = 256;
+constexpr int kNoAllocMaxDim = 4096;
+static __device__ __align__(256) float scratch[kNoAllocParts * kNoAllocMaxDim];  // 4 MiB
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on first use).
+int scratch_on_current_device(float** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return LH_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return LH_ERR_LAUNCH;
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return LH_OK;
+}
+}  // namespace
+
+extern "C" int lh_rmsnorm_bwd_noalloc(const void* dy, const void* x, const void* w, const float* rstd,
+                                      const void* dres, void* dx, void* dw, int64_t rows, int dim, void* stream) {
+  if (!dy || !x || !w || !rstd || !dx || !dw || rows <= 0 || dim <= 0) return LH_ERR_INVALID_ARG;
+  if (dim > kNoAllocMaxDim) return LH_ERR_UNSUPPORTED;
+  float* part = nullptr;
+  const int rc = scratch_on_current_device(&part);
+  if (rc != LH_OK) return rc;
+  return lh_rmsnorm_bwd(dy, x, w, rstd, dres, dx, dw, part, kNoAllocParts, rows, dim, stream);
 }
 
 extern "C" int lh_swiglu_fwd(const void* h, void* a, int64_t rows, int F, void* stream) {
