@@ -43,6 +43,9 @@ WORKLOADS = {
     "cfg3_k6144": dict(B=1, H=8, S=65536, L=3, p=4, topk=6144, strict=False, scorer="norm", heavy_keys=0.05),
     "cfg4": dict(B=1, H=8, S=131072, L=5, p=2, topk=1536, strict=False, scorer="dilated", dilation=4),
     "cfg5_layer": dict(B=1, H=8, S=32768, L=3, p=4, topk=1536, strict=False, scorer="norm"),
+    # the reference's GLA scorer config (configs/scorer/gla.toml: k=2048, p=4, L=3) at the cfg2 shape,
+    # gate logsigmoid(N(0,1)) / 16 as the patch's logsigmoid(wg(x)) / 16
+    "gla": dict(B=1, H=8, S=32768, L=3, p=4, topk=2048, strict=True, scorer="gla", dilation=4),
 }
 D = 128
 # Model workloads: one training step (forward, backward, clip, AdamW) of the Llama3 model.
@@ -65,11 +68,18 @@ def make_inputs(w, torch, device, seed=1234, heads=None):
         pos = torch.randperm(S, device=device, generator=g)[: int(round(w["heavy_keys"] * S))]
         xs[1][:, pos] *= 4.0
     dout = torch.randn(B, H, S, D, device=device, generator=g)
+    gk = None
+    if w["scorer"] == "gla":
+        gk = torch.nn.functional.logsigmoid(torch.randn(B, S, H, device=device, generator=g)) / 16
     if heads is not None:
         hs = torch.as_tensor(heads, device=device)
         xs = [x.index_select(2, hs) for x in xs]
         dout = dout.index_select(1, hs)
-    return [x.bfloat16() for x in xs], dout.bfloat16()
+        gk = gk.index_select(2, hs) if gk is not None else None
+    xs = [x.bfloat16() for x in xs]
+    if gk is not None:
+        return xs, dout.bfloat16(), gk.bfloat16()
+    return xs, dout.bfloat16()
 
 
 def make_layer(w, pkg):
@@ -77,6 +87,9 @@ def make_layer(w, pkg):
     if w["scorer"] == "dilated":
         scorer = pkg.DilatedLighthouseScorer(head_dim=D, dilation=w["dilation"], pooling_factor=w["p"],
                                              levels=w["L"])
+    elif w["scorer"] == "gla":
+        scorer = pkg.DilatedLighthouseGLAScorer(head_dim=D, dilation=w["dilation"], pooling_factor=w["p"],
+                                                levels=w["L"])
     else:
         scorer = pkg.DialatedLighthouseNormScorer(pooling_factor=w["p"], levels=w["L"])
     return pkg.LighthouseLocal(attention=None, scorer=scorer, num_levels=w["L"], pooling_factor=w["p"],
@@ -90,7 +103,7 @@ def algorithmic_work(w, S_sel):
     S_tot = sum(S // p ** l for l in range(L))
     pairs = S_sel * (S_sel + 1) / 2 * B * H  # causal (query, key) pairs
     e = 2
-    if w["scorer"] == "dilated":
+    if w["scorer"] in ("dilated", "gla"):
         # base scores come in (fp32, two tensors); pooled levels of rows and scores go out
         pyr = 3 * S * H * D * e + 3 * (S_tot - S) * H * D * e + 2 * S * H * 4 + 2 * (S_tot - S) * H * 4
     else:
@@ -109,6 +122,11 @@ def algorithmic_work(w, S_sel):
         sd = S // w["dilation"]
         # two dense causal attentions (q->k, k->q) over dil*H virtual heads of length S/dil
         work["dilated_scores"] = ("flop", 2 * 4 * D * (w["dilation"] * H) * sd * (sd + 1) / 2 * B)
+    if w["scorer"] == "gla":
+        # chunked simple GLA, both directions, per 64-token chunk of each virtual head:
+        # Q K^T and A V (64 x 64 x D each), Q H and K^T V (64 x D x D each)
+        chunks = -(-(S // w["dilation"]) // 64) * w["dilation"] * H * B
+        work["gla_scores"] = ("flop", 2 * chunks * 2 * (2 * 64 * 64 * D + 2 * 64 * D * D))
     return work
 
 
@@ -127,15 +145,16 @@ def run_gpu(args, pkg, torch):
     w = WORKLOADS[args.workload]
     B, H, S, L, p, k, strict = (w[n] for n in ("B", "H", "S", "L", "p", "topk", "strict"))
     dev = torch.device("cuda:0")
-    xs, dout = make_inputs(w, torch, dev)
+    xs, dout, *gate = make_inputs(w, torch, dev)
     xs = [x.requires_grad_() for x in xs]
+    kw = {"gk": gate[0]} if gate else {}
     layer = make_layer(w, pkg)
     S_sel = pkg._native.geometry(S, L, p, k, strict)[3]
 
     def step():
         for x in xs:
             x.grad = None
-        out = layer(*xs)
+        out = layer(*xs, **kw)
         out.backward(dout)
 
     for _ in range(args.warmup):
@@ -329,14 +348,16 @@ def run_cpu_baseline(args, torch):
     from oracle import lh_oracle as O
     w = WORKLOADS[args.workload]
     B, H, S, L, p, k, strict = (w[n] for n in ("B", "H", "S", "L", "p", "topk", "strict"))
-    hs = max(1, min(args.cpu_heads if args.cpu_heads else (1 if w["scorer"] == "dilated" else 2), H))
-    xs0, dout = make_inputs(w, torch, torch.device("cpu"), seed=99, heads=list(range(hs)))
+    hs = max(1, min(args.cpu_heads if args.cpu_heads else (1 if w["scorer"] in ("dilated", "gla") else 2), H))
+    xs0, dout, *gate = make_inputs(w, torch, torch.device("cpu"), seed=99, heads=list(range(hs)))
     dout = dout.float()
+    gk = gate[0].float() if gate else None
 
     def run(backward):
         xs = [x.float().requires_grad_(backward) for x in xs0]
         t0 = time.perf_counter()
-        out, _ = O.lighthouse_layer(*xs, L, p, k, scorer=w["scorer"], dilation=w.get("dilation", 4), strict=strict)
+        out, _ = O.lighthouse_layer(*xs, L, p, k, scorer=w["scorer"], dilation=w.get("dilation", 4), strict=strict,
+                                    gk=gk)
         if backward:
             out.backward(dout)
         return time.perf_counter() - t0

@@ -114,6 +114,21 @@ int lh_dilated_scores(const void *xq, const void *xk, const void *xv,
                       int B, int S, int H, int D, int dilation, int S_tot, void *stream);
 
 /*
+ * GLA scorer base scores: the bf16-rounded L2 norms of the two simple gated
+ * linear attention outputs o = chunk_simple_gla(q, k, v, g, scale) and
+ * chunk_simple_gla(k, q, v, g, scale) (each output rounded to bf16 first) over
+ * the dilated virtual heads, written to scores_qk/_kq[:, :, 0:S].
+ * Replaces the two fla chunk_simple_gla calls and norms of
+ * DilatedLighthouseGLAScorer.forward (src/lighthouse_selection.py:713-734).
+ *   xq, xk, xv  bf16 [B, S, H, D] contiguous; gk fp32 [B, S, H] contiguous log gates
+ *   (token t of head h is position t / dilation of virtual head (t % dilation) * H + h)
+ * Then lh_pyramid_fwd with base_scores_given = 1 pools the levels.
+ */
+int lh_gla_scores(const void *xq, const void *xk, const void *xv, const float *gk,
+                  float *scores_qk, float *scores_kq,
+                  int B, int S, int H, int D, int dilation, int S_tot, float scale, void *stream);
+
+/*
  * Hierarchical per-tile top-k selection, emitted in causal order.
  * Replaces lighthouse_selection_chunked_topk_kernel + torch.sort/gather
  * (src/lighthouse_selection_cuda.py:114-331, :399-427).

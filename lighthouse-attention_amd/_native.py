@@ -39,6 +39,7 @@ _SIGS = {
     "lh_pyramid_fwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _P, _P,
                             _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_dilated_scores": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_gla_scores": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P]),
     "lh_select_topk": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_build_inverse": (_I, [_P, _I, _P, _I, _I, _I, _P]),
     "lh_check_indices": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
@@ -281,6 +282,28 @@ def dilated_scores(xq, xk, xv, dilation: int, S_tot: int):
         rc = lib().lh_dilated_scores(_ptr(xq), _ptr(xk), _ptr(xv), _ptr(sqk), _ptr(skq), B, S, H, D, dilation,
                                      S_tot, _stream(dev))
     _check(rc, "lh_dilated_scores")
+    return sqk, skq
+
+
+def gla_scores(xq, xk, xv, gk, dilation: int, S_tot: int, scale: float | None = None):
+    """Base-level GLA scores into fresh fp32 [B, H, S_tot] buffers (pooled levels unset).
+    ``gk`` [B, S, H] log gates (any float dtype; taken in fp32, as fla does)."""
+    _need_rows("gla_scores", xq, xk, xv)
+    _need_gpu(xq, xk, xv, gk)
+    B, S, H, D = xq.shape
+    for t in (xq, xk, xv):
+        assert t.is_contiguous()
+    if tuple(gk.shape) != (B, S, H):
+        raise ValueError(f"gk must be [B, S, H] = {(B, S, H)}, got {tuple(gk.shape)}")
+    g = gk.float().contiguous()
+    dev = xq.device
+    sqk = torch.empty(B, H, S_tot, dtype=torch.float32, device=dev)
+    skq = torch.empty_like(sqk)
+    scale = D ** -0.5 if scale is None else scale
+    with torch.cuda.device(dev):
+        rc = lib().lh_gla_scores(_ptr(xq), _ptr(xk), _ptr(xv), _ptr(g), _ptr(sqk), _ptr(skq), B, S, H, D, dilation,
+                                 S_tot, float(scale), _stream(dev))
+    _check(rc, "lh_gla_scores")
     return sqk, skq
 
 

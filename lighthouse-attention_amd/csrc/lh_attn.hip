@@ -969,6 +969,195 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
     store_rows_bf16(a.dk + ((int64_t)bh * n + my_k) * LH_D, acc, a.scale, hh);
 }
 
+// ===========================================================================
+// GLA scorer: simple gated linear attention over the dilated virtual heads,
+//   o_t = scale * sum_{s <= t} exp(G_t - G_s) (q_t . k_s) v_s,  G = cumsum(g),
+// and the bf16-rounded L2 norm of the bf16-rounded o_t as the base score.
+// Chunked form (chunks of 64 tokens, processed in order): with b the
+// chunk-local inclusive cumsum of g and H the state after the previous chunk,
+//   o = scale * ((Q K^T) o exp(b_t - b_s), causal) V + scale * exp(b_t) Q H
+//   H <- exp(b_last) H + (K o exp(b_last - b_s))^T V.
+// One workgroup (8 waves) owns one (b, virtual head, direction).  The state is
+// kept transposed, H^T [j][i] (j: value dim, i: key dim), in fp32 MFMA
+// accumulators (wave w: rows 32 (w >> 1), columns 64 (w & 1) .. + 63) with a bf16
+// copy in LDS as the operand of the inter-chunk product.  As in the forward
+// kernel, products come out transposed (A^T, O^T), so an accumulator column is
+// a token.  Per chunk: phase 1 (waves 0-2) forms the three causal 32x32 blocks
+// of A^T and hands them over in LDS as packed bf16 operands, wave 3 the decay
+// factors; phase 2 every wave forms one 32-token x 32-column block of O^T
+// (norm partials to LDS) and updates its state blocks; phase 3 writes the new
+// bf16 state copy and wave 0 finishes the norms.  Tiles of the next chunk are
+// loaded (direct global->LDS) during the current one.
+// ===========================================================================
+struct GlaArgs {
+  const bf16_t *q, *k, *v;  // [B, S, H, D] contiguous
+  const float* g;           // [B, S, H] fp32 log gates
+  float *sqk, *skq;         // [B, H, S_tot]: base level written
+  int B, S, H, dil, T, S_tot;
+  float scale;
+};
+
+__device__ __forceinline__ void gla_issue(bf16_t* tile, const bf16_t* base, uint32_t stride, int t0, int last,
+                                          int w, int lane) {
+  const int rsub = lane >> 4, slot = lane & 15;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = 8 * w + 4 * i + rsub;
+    const int t = min(t0 + r, last);
+    g2l16(base + (uint32_t)t * stride + 8 * (slot ^ swz(r)), tile + (8 * w + 4 * i) * LH_D);
+  }
+}
+
+// bf16 element (row, col) of a swizzled 64 x 128 tile
+__device__ __forceinline__ int tile_elem(int row, int col) { return row * LH_D + ((((col >> 3) ^ swz(row)) << 3) | (col & 7)); }
+
+__global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
+  __shared__ __attribute__((aligned(1024))) bf16_t Qt[2][TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t Kt[2][TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t Vt[2][TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t HT[2][TILE];  // bf16 H^T: rows j, columns i
+  __shared__ __attribute__((aligned(16))) float Gs[2][64];
+  __shared__ __attribute__((aligned(16))) float Es[64], Fs[64];  // exp(b_t), exp(b_last - b_s) (0 past the end)
+  __shared__ u32x4 AP[3][2][64];                                  // packed A^T blocks (s0,t0), (s0,t1), (s1,t1)
+  __shared__ float RED[4][64];                                    // norm partials per column block
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const LaneLds ll = lane_lds(lane);
+  const int VH = a.dil * a.H;
+  const int dir = blockIdx.x & 1;
+  const int seq = blockIdx.x >> 1;
+  const int b = seq / VH, vh = seq % VH;
+  const int r = vh / a.H, ho = vh % a.H;
+  const uint32_t stride = (uint32_t)VH * LH_D;  // elements between consecutive tokens of a virtual head
+  const int64_t off = (int64_t)b * a.S * a.H * LH_D + (int64_t)vh * LH_D;
+  const bf16_t* qb = (dir ? a.k : a.q) + off;
+  const bf16_t* kb = (dir ? a.q : a.k) + off;
+  const bf16_t* vb = a.v + off;
+  const float* gb = a.g + (int64_t)b * a.S * a.H + vh;
+  float* scores = (dir ? a.skq : a.sqk) + ((int64_t)b * a.H + ho) * a.S_tot + r;
+  const int T = a.T, last = T - 1;
+  const int nch = (T + 63) / 64;
+  const float L2E = 1.4426950408889634f;
+
+  // zero state copy
+  for (int e = tid; e < 2 * TILE / 8; e += 512) reinterpret_cast<u32x4*>(&HT[0][0])[e] = u32x4{0, 0, 0, 0};
+  floatx16 hs[2] = {floatx16{}, floatx16{}};
+  const int sjb = w >> 1, sib = 2 * (w & 1);  // state blocks (j block, i blocks sib, sib + 1)
+  const int otb = w & 1, odb = w >> 1;         // output block (token block, column block)
+
+  auto issue = [&](int c, int buf) {
+    const int t0 = 64 * c;
+    gla_issue(Qt[buf], qb, stride, t0, last, w, lane);
+    gla_issue(Kt[buf], kb, stride, t0, last, w, lane);
+    gla_issue(Vt[buf], vb, stride, t0, last, w, lane);
+    if (w == 0) g2l4(gb + (int64_t)min(t0 + lane, last) * VH, Gs[buf]);
+  };
+  issue(0, 0);
+  wait_loads();
+  __syncthreads();
+
+  for (int c = 0; c < nch; ++c) {
+    const int buf = c & 1;
+    const int nvalid = min(64, T - 64 * c);
+    if (c + 1 < nch) issue(c + 1, buf ^ 1);
+    // ---- phase 1: A^T blocks (waves 0-2), decay factors (wave 3)
+    if (w < 4) {
+      // chunk-local inclusive cumsum of g (log2 units); tokens past the end add 0
+      float x = (lane < nvalid) ? Gs[buf][lane] * L2E : 0.f;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const float y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+      }
+      if (w == 3) {
+        const float bl = __shfl(x, nvalid - 1);
+        Es[lane] = ex2(x);
+        Fs[lane] = lane < nvalid ? ex2(bl - x) : 0.f;
+      } else {
+        const int tb = w == 0 ? 0 : 1, sbk = w == 2 ? 1 : 0;
+        floatx16 acc = floatx16{};
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc)
+          acc = mfma(lds_row(Kt[buf], ll, sbk, cc), lds_row(Qt[buf], ll, tb, cc), acc);
+        const int t = 32 * tb + l32;
+        const float bt = __shfl(x, t);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int s = 32 * sbk + slot_key(v, hh);
+          const float bs = __shfl(x, s);
+          acc[v] = (s <= t && s < nvalid) ? acc[v] * a.scale * ex2(bt - bs) : 0.f;
+        }
+        AP[w][0][lane] = pack_frag(acc, 0);
+        AP[w][1][lane] = pack_frag(acc, 1);
+      }
+    }
+    __syncthreads();
+    // ---- phase 2: O^T block (otb, odb) and the state update
+    {
+      floatx16 oi = floatx16{}, oa = floatx16{};
+      // inter-chunk: H^T rows of column block odb against the chunk's queries
+#pragma unroll
+      for (int cc = 0; cc < 8; ++cc)
+        oi = mfma(lds_row(HT[odb >> 1], ll, odb & 1, cc), lds_row(Qt[buf], ll, otb, cc), oi);
+      // intra-chunk: V^T against the packed A^T blocks of this token block
+#pragma unroll
+      for (int sbk = 0; sbk < 2; ++sbk) {
+        if (sbk > otb) break;
+        const int blk = otb == 0 ? 0 : 1 + sbk;
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) oa = mfma(lds_tr(Vt[buf], ll, 32 * sbk + 16 * c2, odb), AP[blk][c2][lane], oa);
+      }
+      const float et = Es[32 * otb + l32] * a.scale;
+      float ss = 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float o = fmaf(oi[v], et, oa[v]);
+        const float ob = __uint_as_float(cvt2(o, 0.f) << 16);  // the bf16 output value
+        ss = fmaf(ob, ob, ss);
+      }
+      ss += __shfl_xor(ss, 32);
+      if (hh == 0) RED[odb][32 * otb + l32] = ss;
+      // state: H^T <- exp(b_last) H^T + (V o f)^T K
+      const float el = Es[nvalid - 1];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) hs[q] *= el;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        u32x4 vt = lds_tr(Vt[buf], ll, 16 * kk, sjb);
+        const float4 f0 = *reinterpret_cast<const float4*>(&Fs[16 * kk + 4 * hh]);
+        const float4 f1 = *reinterpret_cast<const float4*>(&Fs[16 * kk + 8 + 4 * hh]);
+        const float fv[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = __uint_as_float(vt[e] << 16) * fv[2 * e];
+          const float hi = __uint_as_float(vt[e] & 0xffff0000u) * fv[2 * e + 1];
+          vt[e] = cvt2(lo, hi);
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) hs[q] = mfma(vt, lds_tr(Kt[buf], ll, 16 * kk, sib + q), hs[q]);
+      }
+    }
+    __syncthreads();
+    // ---- phase 3: bf16 copy of the new state; norms of this chunk
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = 32 * (sib + q) + l32;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int j = 32 * sjb + slot_key(v, hh);
+        HT[j >> 6][tile_elem(j & 63, i)] = (bf16_t)(cvt2(hs[q][v], 0.f) & 0xffffu);
+      }
+    }
+    if (w == 7 && lane < nvalid) {
+      const float ss = (RED[0][lane] + RED[1][lane]) + (RED[2][lane] + RED[3][lane]);
+      const uint32_t nb = cvt2(sqrtf(ss), 0.f) << 16;
+      scores[(int64_t)(64 * c + lane) * a.dil] = __uint_as_float(nb);
+    }
+    wait_loads();
+    __syncthreads();
+  }
+}
+
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int fill_rows(AttnArgs& a, const void* q, const void* k, const void* v, int64_t sb, int64_t ss, int64_t sh,
@@ -1096,5 +1285,25 @@ extern "C" int lh_dilated_scores(const void* xq, const void* xk, const void* xv,
     hipLaunchKernelGGL(attn_fwd_kernel<1>, dim3(a.nq * a.BH), dim3(64 * QW), 0, st, a);
     LH_CHECK_LAUNCH();
   }
+  return LH_OK;
+}
+
+extern "C" int lh_gla_scores(const void* xq, const void* xk, const void* xv, const float* gk, float* scores_qk,
+                             float* scores_kq, int B, int S, int H, int D, int dilation, int S_tot, float scale,
+                             void* stream) {
+  if (D != LH_D) return LH_ERR_UNSUPPORTED;
+  if (!xq || !xk || !xv || !gk || !scores_qk || !scores_kq || B <= 0 || H <= 0 || dilation <= 0 || S <= 0 ||
+      S % dilation || S_tot < S || !(scale > 0.f))
+    return LH_ERR_INVALID_ARG;
+  if (!al16(xq) || !al16(xk) || !al16(xv) || (reinterpret_cast<uintptr_t>(gk) & 3u)) return LH_ERR_INVALID_ARG;
+  // token offsets inside one virtual head are 32-bit
+  if ((long long)S * H * D > 0x7fffffffLL || (long long)B * dilation * H * 2 > 0x7fffffffLL) return LH_ERR_UNSUPPORTED;
+  GlaArgs a{};
+  a.q = (const bf16_t*)xq; a.k = (const bf16_t*)xk; a.v = (const bf16_t*)xv; a.g = gk;
+  a.sqk = scores_qk; a.skq = scores_kq;
+  a.B = B; a.S = S; a.H = H; a.dil = dilation; a.T = S / dilation; a.S_tot = S_tot; a.scale = scale;
+  hipLaunchKernelGGL(gla_scores_kernel, dim3(B * dilation * H * 2), dim3(512), 0,
+                     reinterpret_cast<hipStream_t>(stream), a);
+  LH_CHECK_LAUNCH();
   return LH_OK;
 }

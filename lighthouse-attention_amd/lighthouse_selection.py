@@ -11,7 +11,7 @@ name here                           reference
 ==================================  =====================================================
 ``DialatedLighthouseNormScorer``    ``src/lighthouse_selection.py:578-616``
 ``DilatedLighthouseScorer``         ``src/lighthouse_selection.py:618-689``
-``DilatedLighthouseGLAScorer``      ``src/lighthouse_selection.py:692-755`` (not built)
+``DilatedLighthouseGLAScorer``      ``src/lighthouse_selection.py:692-755``
 ``LighthouseLocal``                 ``src/lighthouse_selection.py:772-825``
 ``scatter_to_base_sequence``        ``src/lighthouse_selection.py:758-770``
 ``DialatedLighthouseNormScorerCP``  ``src/lighthouse_selection.py:943-982`` (not built)
@@ -32,6 +32,9 @@ Differences from the reference, all deliberate:
   * ``DilatedLighthouseScorer``'s ``attention`` is optional and ``head_dim`` is
     accepted, so the reference's own builder call (``lighthouse-attention.patch:623-628``)
     constructs it.
+  * ``LighthouseLocal.forward`` takes the GLA scorer's gate as ``gk`` (the
+    reference's caller passes it, lighthouse-attention.patch:709-710, but the
+    reference's ``LighthouseLocal.forward`` has no such parameter).
 """
 from __future__ import annotations
 
@@ -116,15 +119,21 @@ def _mark(name):
         _op_hook(name)
 
 
-def _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major):
+def _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk=None):
     """Forward of the whole layer on contiguous bf16 [B, S, H, D] inputs:
-    pyramid -> selection -> gathered causal attention -> fan-out.  Returns
-    ``(out, idx, saved)`` with ``saved = (pq, pk, pv, inv, o, lse)``."""
+    pyramid -> selection -> gathered causal attention -> fan-out.  The scorer is
+    the norm scorer (dilation 0), the dilated one (dilation > 0) or, with the gate
+    ``gk`` [B, S, H], the GLA one.  Returns ``(out, idx, saved)`` with
+    ``saved = (pq, pk, pv, inv, o, lse)``."""
     B, S, H, D = xq.shape
     _, _, S_tot = N.pyramid_lengths(S, L, p)
     _, _, _, S_sel = N.geometry(S, L, p, topk, strict)
     _mark("fwd_start")
-    if dilation:
+    if gk is not None:
+        scores = N.gla_scores(xq, xk, xv, gk, dilation, S_tot)
+        _mark("gla_scores")
+        pq, pk, pv, sqk, skq = N.pyramid_fwd(xq, xk, xv, L, p, scores=scores)
+    elif dilation:
         scores = N.dilated_scores(xq, xk, xv, dilation, S_tot)
         _mark("dilated_scores")
         pq, pk, pv, sqk, skq = N.pyramid_fwd(xq, xk, xv, L, p, scores=scores)
@@ -168,10 +177,10 @@ class _LighthouseLayerFn(torch.autograd.Function):
     """Whole layer (``_layer_fwd`` / ``_layer_bwd``) as one autograd node."""
 
     @staticmethod
-    def forward(ctx, xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major):
+    def forward(ctx, xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk):
         xq, xk, xv = xq.contiguous(), xk.contiguous(), xv.contiguous()
         out, idx, (pq, pk, pv, inv, o, lse) = _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation,
-                                                         seq_major)
+                                                         seq_major, gk)
         ctx.save_for_backward(xq, xk, xv, pq, pk, pv, idx, inv, o, lse)
         ctx.geo = (L, p)
         ctx.mark_non_differentiable(idx)
@@ -181,17 +190,19 @@ class _LighthouseLayerFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout, _didx):
         if dout is None:
-            return (None,) * 10
+            return (None,) * 11
         dx = _layer_bwd(dout, *ctx.saved_tensors, *ctx.geo)
-        return dx + (None,) * 7
+        return dx + (None,) * 8  # the gate gets no gradient: the scores only feed the selection
 
 
 def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, topk: int = 1024,
                      tie_break: str = "reference", strict: bool = True, dilation: int = 0,
-                     seq_major: bool = False):
+                     seq_major: bool = False, gk=None):
     """Functional form of the native layer: ``(out [B, H, S, D], indices [B, H, S_sel])``.
 
-    ``dilation > 0`` selects the dilated scorer, 0 the norm scorer.  ``seq_major``
+    ``dilation > 0`` selects the dilated scorer, 0 the norm scorer; a gate ``gk``
+    [B, S, H] (log gates) selects the GLA scorer over ``dilation`` virtual heads per
+    head (the gate receives no gradient, as in the reference).  ``seq_major``
     stores ``out`` as ``[B, S, H, D]`` (the returned tensor is its ``[B, H, S, D]``
     view), which is the layout the model's output projection reads.  Under
     ``torch.compile`` the layer is one registered custom op (traced without a
@@ -205,12 +216,16 @@ def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, t
             raise TypeError("the native layer computes in bfloat16; got " + str(t.dtype))
     if tie_break not in N.TIE_MODES:
         raise ValueError(f"tie_break must be one of {sorted(N.TIE_MODES)}, got {tie_break!r}")
+    if gk is not None:
+        if dilation <= 0:
+            raise ValueError("the GLA scorer needs dilation >= 1")
+        gk = gk.detach()
     if torch.compiler.is_compiling():
         out, idx = _compiled_ops.layer_fwd(xq, xk, xv, num_levels, pooling_factor, topk, tie_break, bool(strict),
-                                           int(dilation), bool(seq_major))[:2]
+                                           int(dilation), bool(seq_major), gk)[:2]
         return out, idx
     return _LighthouseLayerFn.apply(xq, xk, xv, num_levels, pooling_factor, topk, tie_break, strict,
-                                    int(dilation), bool(seq_major))
+                                    int(dilation), bool(seq_major), gk)
 
 
 def _rope_layer_fwd(xqkv, freqs, H, L, p, topk, tie, strict, seq_major):
@@ -328,14 +343,14 @@ class _CompiledOps:
 
         @torch.library.custom_op(f"{lib}::layer_fwd", mutates_args=(), schema=(
             "(Tensor xq, Tensor xk, Tensor xv, int L, int p, int topk, str tie, bool strict, int dilation, "
-            "bool seq_major) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)"))
-        def layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major):
+            "bool seq_major, Tensor? gk) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)"))
+        def layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk):
             xq, xk, xv = xq.contiguous(), xk.contiguous(), xv.contiguous()
-            out, idx, saved = _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major)
+            out, idx, saved = _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk)
             return (out, idx) + saved
 
         @layer_fwd.register_fake
-        def _(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major):
+        def _(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk):
             B, S, H, D = xq.shape
             _, _, S_tot = N.pyramid_lengths(S, L, p)
             S_sel = N.geometry(S, L, p, topk, strict)[3]
@@ -363,10 +378,10 @@ class _CompiledOps:
 
         def layer_grad(ctx, dout, *_unused):
             if dout is None:
-                return (None,) * 10
+                return (None,) * 11
             xq, xk, xv, pq, pk, pv, idx, inv, o, lse = ctx.saved_tensors
             dx = layer_bwd(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, *ctx.geo)
-            return tuple(dx) + (None,) * 7
+            return tuple(dx) + (None,) * 8
 
         layer_fwd.register_autograd(layer_grad, setup_context=layer_setup)
 
@@ -591,8 +606,13 @@ class DilatedLighthouseScorer(nn.Module):
 
 
 class DilatedLighthouseGLAScorer(nn.Module):
-    """Name kept for the reference's imports (``src/lighthouse_selection.py:692-755``).
-    The GLA scorer needs the ``fla`` package and is not part of this build."""
+    """GLA scorer (``src/lighthouse_selection.py:692-755``): the scores are the L2
+    norms of two simple gated linear attentions (q->k and k->q, both with v) over
+    the dilated virtual heads, gated by ``gk`` [B, S, H] (log gates, e.g.
+    ``logsigmoid(wg(x)) / 16``, lighthouse-attention.patch:709), computed by the
+    native chunked GLA kernel (the reference calls ``fla``'s ``chunk_simple_gla``).
+    Calling it returns the reference's 5-tuple; ``LighthouseLocal`` uses the fused
+    native path instead."""
 
     def __init__(self, head_dim: int, dilation: int = 4, pooling_factor: int = 4, levels: int = 3):
         super().__init__()
@@ -603,8 +623,12 @@ class DilatedLighthouseGLAScorer(nn.Module):
         self.scaling = 1.0 / math.sqrt(head_dim)
 
     def forward(self, xq, xk, xv, gk):
-        raise RuntimeError("lighthouse_scorer='gla' requires the `fla` package, which this MI355X build does "
-                           "not include; use 'norm' or 'dilated'.")
+        b, s, h, d = xq.shape
+        _, _, S_tot = N.pyramid_lengths(s, self.levels, self.pooling_factor)
+        with torch.no_grad():
+            sqk, skq = N.gla_scores(xq.contiguous(), xk.contiguous(), xv.contiguous(), gk.detach(), self.dilation,
+                                    S_tot, self.scaling)
+        return _PyramidCatFn.apply(xq, xk, xv, self.levels, self.pooling_factor, 0, sqk[..., :s], skq[..., :s])
 
 
 class LighthouseLocal(nn.Module):
@@ -634,6 +658,8 @@ class LighthouseLocal(nn.Module):
             return 0
         if type(sc) is DilatedLighthouseScorer and sc.attention is None:
             return sc.dilation
+        if type(sc) is DilatedLighthouseGLAScorer and sc.head_dim == N.D_SUPPORTED:  # native scale 1/sqrt(D)
+            return sc.dilation
         return None
 
     def fuses_rope(self) -> bool:
@@ -652,17 +678,24 @@ class LighthouseLocal(nn.Module):
         self.last_indices = idx
         return out
 
-    def forward(self, xq, xk, xv):
+    def forward(self, xq, xk, xv, gk=None):
+        """``gk`` [B, S, H]: the gate of the GLA scorer (required with it, unused
+        otherwise); the reference's caller passes it as ``selection_attn(xq, xk,
+        xv, gk=gk)`` (lighthouse-attention.patch:709-710)."""
         _, s, _, d = xq.shape
+        gla = isinstance(self.scorer, DilatedLighthouseGLAScorer)
+        if gla and gk is None:
+            raise ValueError("the GLA scorer needs the gate gk ([B, S, H] log gates)")
         dil = self._native_dilation()
         if self.use_native_attention and dil is not None and \
                 self.scorer.levels == self.num_levels and self.scorer.pooling_factor == self.pooling_factor:
             out, idx = lighthouse_layer(xq, xk, xv, self.num_levels, self.pooling_factor, self.topk,
-                                        self.tie_break, self.strict, dil, self.out_seq_major)
+                                        self.tie_break, self.strict, dil, self.out_seq_major,
+                                        gk if gla else None)
             self.last_indices = idx
             return out
         # generic composition, as in the reference, for scorers and attentions from elsewhere
-        sqk, skq, xq_cat, xk_cat, xv_cat = self.scorer(xq, xk, xv)
+        sqk, skq, xq_cat, xk_cat, xv_cat = self.scorer(xq, xk, xv, gk) if gla else self.scorer(xq, xk, xv)
         with torch.no_grad():
             idx = LighthouseSelectionQkKqChunkedTopkHip.forward(
                 sqk.to(torch.float32), skq.to(torch.float32), self.num_levels, self.pooling_factor, self.topk, s,

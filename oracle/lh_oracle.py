@@ -18,6 +18,9 @@ function here                          reference it restates
 ``select_indices``                     ``src/lighthouse_selection_cuda.py:114-331,399-427``
 ``norm_scorer``                        ``src/lighthouse_selection.py:589-616``
 ``dilated_scorer``                     ``src/lighthouse_selection.py:635-689``
+``gla_scorer``, ``simple_gla``         ``src/lighthouse_selection.py:692-755`` (+ fla's
+                                       ``chunk_simple_gla``, restated from its
+                                       published recurrence)
 ``sdpa_causal``                        ``src/lighthouse_selection.py:815`` (causal SDPA)
 ``scatter_fwd`` / ``scatter_bwd``      ``src/lighthouse_selection.py:408-514,517-576``
 ``lighthouse_layer``                   ``src/lighthouse_selection.py:789-825``
@@ -484,6 +487,80 @@ def dilated_scorer(xq, xk, xv, dilation: int = 4, pooling_factor: int = 4, level
     return cat(al), cat(bl), cat(ql), cat(kl), cat(vl)
 
 
+def simple_gla(q, k, v, g, scale: float):
+    """Simple gated linear attention, quadratic form: for each head of
+    ``[B, T, H, D]`` inputs and log gates ``g`` ``[B, T, H]``,
+    ``o_t = scale * sum_{s <= t} exp(G_t - G_s) (q_t . k_s) v_s`` with
+    ``G = cumsum(g)`` along T.  This is the output of ``fla``'s
+    ``chunk_simple_gla(q, k, v, g, scale)`` (flash-linear-attention 0.4.x,
+    pinned by ``requirements.txt``; not vendored with the reference), i.e. the
+    recurrence ``h_t = exp(g_t) h_{t-1} + k_t^T v_t``, ``o_t = scale q_t h_t``
+    from a zero state.  Computed in float64."""
+    qd, kd, vd = (x.double().transpose(1, 2) for x in (q, k, v))  # [B, H, T, D]
+    G = torch.cumsum(g.double().transpose(1, 2), dim=-1)          # [B, H, T]
+    T = qd.shape[2]
+    diff = G[..., :, None] - G[..., None, :]                        # G_t - G_s
+    causal = torch.ones(T, T, dtype=torch.bool).tril()
+    decay = torch.where(causal, torch.exp(torch.where(causal, diff, torch.zeros_like(diff))),
+                        torch.zeros_like(diff))
+    a = (qd @ kd.transpose(-1, -2)) * decay * scale
+    return (a @ vd).transpose(1, 2)                                  # [B, T, H, D]
+
+
+def simple_gla_recurrent(q, k, v, g, scale: float):
+    """The same output by the token-by-token recurrence (float64, tiny shapes)."""
+    B, T, H, D = q.shape
+    out = torch.zeros(B, T, H, D, dtype=torch.float64)
+    for b in range(B):
+        for hd in range(H):
+            st = torch.zeros(D, D, dtype=torch.float64)
+            for t in range(T):
+                st = math.exp(float(g[b, t, hd])) * st + torch.outer(k[b, t, hd].double(), v[b, t, hd].double())
+                out[b, t, hd] = scale * (q[b, t, hd].double() @ st)
+    return out
+
+
+def gla_scorer(xq, xk, xv, gk, dilation: int = 4, pooling_factor: int = 4, levels: int = 3,
+               scale: float | None = None, round_bf16: bool = False):
+    """``DilatedLighthouseGLAScorer.forward`` (``src/lighthouse_selection.py:713-755``).
+
+    Token t of head h is position ``t // dil`` of virtual head ``(t % dil) * H + h``
+    (the reference's ``.view(b, s // dil, dil * h, d)``, :722-725); the scores are the
+    L2 norms of two simple-GLA outputs over those virtual heads, q->k and k->q, both
+    with v and the gate ``gk`` [B, S, H] viewed the same way (:727-734).  The Q/K/V
+    pyramid and the max-pooled score levels are the norm scorer's (:736-755).
+    ``round_bf16`` rounds the GLA outputs to bfloat16 before the norm and the norm
+    after it, as the reference's bf16 tensors do."""
+    b, s, h, d = xq.shape
+    sd = s // dilation
+    scale = d ** -0.5 if scale is None else scale
+
+    def virt(x):
+        return x.reshape(b, sd, dilation * h, *x.shape[3:])
+
+    g = gk.float().reshape(b, sd, dilation * h)
+    with torch.no_grad():
+        o_qk = simple_gla(virt(xq), virt(xk), virt(xv), g, scale).reshape(b, s, h, d)
+        o_kq = simple_gla(virt(xk), virt(xq), virt(xv), g, scale).reshape(b, s, h, d)
+        if round_bf16:
+            o_qk, o_kq = o_qk.bfloat16().double(), o_kq.bfloat16().double()
+        sqk = torch.linalg.vector_norm(o_qk, dim=-1).float()
+        skq = torch.linalg.vector_norm(o_kq, dim=-1).float()
+        if round_bf16:
+            sqk, skq = sqk.bfloat16().float(), skq.bfloat16().float()
+    ql, kl, vl, al, bl = [xq], [xk], [xv], [sqk], [skq]
+    for level in range(1, levels):
+        pf = pooling_factor ** level
+        n = s // pf
+        ql.append(xq[:, :n * pf].reshape(b, n, pf, h, d).mean(2))
+        kl.append(xk[:, :n * pf].reshape(b, n, pf, h, d).mean(2))
+        vl.append(xv[:, :n * pf].reshape(b, n, pf, h, d).mean(2))
+        al.append(sqk[:, :n * pf].reshape(b, n, pf, h).amax(2))
+        bl.append(skq[:, :n * pf].reshape(b, n, pf, h).amax(2))
+    cat = lambda xs: torch.cat(xs, dim=1).transpose(1, 2)  # noqa: E731
+    return cat(al), cat(bl), cat(ql), cat(kl), cat(vl)
+
+
 def fanout_spans(indices, S: int, L: int, p: int):
     """For each selected entry: (first base position, fan-out c_l) of the span
     it is added to, ``[(i+1)c_l - 1, (i+2)c_l - 2]`` clipped to ``[0, S)``
@@ -553,7 +630,7 @@ class _ScatterFn(torch.autograd.Function if torch is not None else object):
 
 def lighthouse_layer(xq, xk, xv, num_levels: int, pooling_factor: int, topk: int,
                      scorer: str = "norm", dilation: int = 4, indices=None,
-                     tie: str = "reference", strict: bool = True):
+                     tie: str = "reference", strict: bool = True, gk=None):
     """``LighthouseLocal.forward`` (``src/lighthouse_selection.py:789-825``) on
     the CPU, differentiable through torch autograd.
 
@@ -567,6 +644,8 @@ def lighthouse_layer(xq, xk, xv, num_levels: int, pooling_factor: int, topk: int
         sqk, skq, qc, kc, vc = norm_scorer(xq, xk, xv, p, L)
     elif scorer == "dilated":
         sqk, skq, qc, kc, vc = dilated_scorer(xq, xk, xv, dilation, p, L)
+    elif scorer == "gla":
+        sqk, skq, qc, kc, vc = gla_scorer(xq, xk, xv, gk, dilation, p, L)
     else:
         raise ValueError(scorer)
     if indices is None:

@@ -135,8 +135,12 @@ def test_reference_import_names_and_constructors(pkg):
     layer = pkg.LighthouseLocal(scorer=norm, num_levels=3, pooling_factor=4, topk=2048, attention=None)
     assert layer.topk == 2048 and layer.tie_break == "reference" and layer.strict
     gla = pkg.DilatedLighthouseGLAScorer(head_dim=128)
-    with pytest.raises(RuntimeError, match="fla"):
-        gla(None, None, None, None)
+    assert gla.dilation == 4 and abs(gla.scaling - 128 ** -0.5) < 1e-12
+    x = torch.zeros(1, 64, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(pkg._native.LighthouseHipError):  # no CPU path
+        gla(x, x, x, torch.zeros(1, 64, 2))
+    with pytest.raises(ValueError, match="gate"):  # the GLA scorer needs its gate
+        pkg.LighthouseLocal(scorer=gla, num_levels=3, pooling_factor=4, topk=128, attention=None)(x, x, x)
     cp = pkg.LighthouseCP(attention=None, scorer=pkg.DialatedLighthouseNormScorerCP())
     cp.set_cp_info(0, 2, None)
     with pytest.raises(NotImplementedError):

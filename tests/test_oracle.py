@@ -458,3 +458,48 @@ def test_select_ref_under_sanitizers(asan_driver, tmp_path, geo, tie):
     assert "runtime error" not in r.stderr and "AddressSanitizer" not in r.stderr, r.stderr[-2000:]
     got = np.fromfile(fo, dtype=np.int32).reshape(1, H, n)
     assert np.array_equal(got, expect)
+
+
+# ----------------------------------------------------------------------------- GLA scorer
+@pytest.mark.parametrize("seed,gscale", [(0, 1.0), (1, 0.05), (2, 8.0)])
+def test_simple_gla_matches_recurrence(seed, gscale):
+    """Quadratic form == token-by-token recurrence h_t = e^{g_t} h_{t-1} + k_t^T v_t."""
+    g0 = torch.Generator().manual_seed(seed)
+    B, T, H, D = 2, 13, 3, 5
+    q, k, v = (torch.randn(B, T, H, D, generator=g0) for _ in range(3))
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=g0) * gscale)
+    a = O.simple_gla(q, k, v, g, 0.37)
+    r = O.simple_gla_recurrent(q, k, v, g, 0.37)
+    assert torch.allclose(a, r, rtol=1e-10, atol=1e-12)
+
+
+def test_simple_gla_limits():
+    """g = 0: causal linear attention, o_t = scale q_t sum_{s<=t} k_s^T v_s (prefix sum
+    of outer products); g -> -inf: only the diagonal survives, o_t = scale (q_t.k_t) v_t."""
+    g0 = torch.Generator().manual_seed(5)
+    B, T, H, D = 1, 17, 2, 6
+    q, k, v = (torch.randn(B, T, H, D, generator=g0, dtype=torch.float64) for _ in range(3))
+    kv = torch.cumsum(k[..., :, None] * v[..., None, :], dim=1)          # [B, T, H, D, D]
+    want = 0.5 * torch.einsum("bthi,bthij->bthj", q, kv)
+    assert torch.allclose(O.simple_gla(q, k, v, torch.zeros(B, T, H), 0.5), want, rtol=1e-10, atol=1e-10)
+    diag = 0.5 * (q * k).sum(-1, keepdim=True) * v
+    assert torch.allclose(O.simple_gla(q, k, v, torch.full((B, T, H), -1e4), 0.5), diag, rtol=1e-10, atol=1e-10)
+
+
+def test_gla_scorer_virtual_heads():
+    """Base scores: token t of head h belongs to the sequence x[:, t % dil :: dil, h]
+    (virtual head (t % dil) * H + h), built here by slicing, not by the reshape."""
+    g0 = torch.Generator().manual_seed(7)
+    B, S, H, D, dil = 2, 48, 3, 8, 4
+    xq, xk, xv = (torch.randn(B, S, H, D, generator=g0) for _ in range(3))
+    gk = torch.nn.functional.logsigmoid(torch.randn(B, S, H, generator=g0)) / 16
+    sqk, skq, *_ = O.gla_scorer(xq, xk, xv, gk, dil, 2, 3)
+    for r in range(dil):
+        for h in range(H):
+            sl = lambda x: x[:, r::dil, h:h + 1]  # noqa: E731
+            oq = O.simple_gla_recurrent(sl(xq), sl(xk), sl(xv), sl(gk), D ** -0.5)
+            ok = O.simple_gla_recurrent(sl(xk), sl(xq), sl(xv), sl(gk), D ** -0.5)
+            assert torch.allclose(sqk[:, h, r:S:dil], oq.norm(dim=-1)[..., 0].float(), rtol=1e-5, atol=1e-6)
+            assert torch.allclose(skq[:, h, r:S:dil], ok.norm(dim=-1)[..., 0].float(), rtol=1e-5, atol=1e-6)
+    # pooled levels: max of the base scores over each span, as the norm scorer's
+    assert torch.equal(sqk[:, :, S:S + S // 2], sqk[:, :, :S].reshape(B, H, S // 2, 2).amax(-1))
