@@ -108,10 +108,12 @@ int lh_rope_pyramid_fwd(const void *xq, const void *xk, const void *xv,
  * over the dilated virtual heads, written to scores_qk/_kq[:, :, 0:S].
  * Replaces the two SDPA calls and norms of DilatedLighthouseScorer.forward
  * (src/lighthouse_selection.py:638-653).  Inputs are contiguous [B, S, H, D].
+ * scale: the softmax scale (<= 0: 1/sqrt(D)); a head dim padded with zeros to D
+ * passes 1/sqrt(its own width).
  */
 int lh_dilated_scores(const void *xq, const void *xk, const void *xv,
                       float *scores_qk, float *scores_kq,
-                      int B, int S, int H, int D, int dilation, int S_tot, void *stream);
+                      int B, int S, int H, int D, int dilation, int S_tot, float scale, void *stream);
 
 /*
  * GLA scorer base scores: the bf16-rounded L2 norms of the two simple gated

@@ -38,7 +38,7 @@ _SIGS = {
     "lh_select_geometry": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P]),
     "lh_pyramid_fwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _P, _P,
                             _I, _I, _I, _I, _I, _I, _I, _P]),
-    "lh_dilated_scores": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_dilated_scores": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P]),
     "lh_gla_scores": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P]),
     "lh_select_topk": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_build_inverse": (_I, [_P, _I, _P, _I, _I, _I, _P]),
@@ -269,7 +269,7 @@ def rope_pyramid_fwd(xqkv, freqs, H: int, L: int, p: int, D: int = D_SUPPORTED):
     return xr, pq, pk, pv, sqk, skq
 
 
-def dilated_scores(xq, xk, xv, dilation: int, S_tot: int):
+def dilated_scores(xq, xk, xv, dilation: int, S_tot: int, scale: float | None = None):
     """Base-level dilated scores into fresh fp32 [B, H, S_tot] buffers (pooled levels unset)."""
     _need_gpu(xq, xk, xv)
     B, S, H, D = xq.shape
@@ -280,7 +280,7 @@ def dilated_scores(xq, xk, xv, dilation: int, S_tot: int):
     skq = torch.empty_like(sqk)
     with torch.cuda.device(dev):
         rc = lib().lh_dilated_scores(_ptr(xq), _ptr(xk), _ptr(xv), _ptr(sqk), _ptr(skq), B, S, H, D, dilation,
-                                     S_tot, _stream(dev))
+                                     S_tot, float(scale or 0.0), _stream(dev))
     _check(rc, "lh_dilated_scores")
     return sqk, skq
 

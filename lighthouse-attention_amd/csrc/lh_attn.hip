@@ -1265,7 +1265,7 @@ extern "C" int lh_attn_bwd_dq(const void* q, const void* k, const void* v, int64
 }
 
 extern "C" int lh_dilated_scores(const void* xq, const void* xk, const void* xv, float* scores_qk, float* scores_kq,
-                                 int B, int S, int H, int D, int dilation, int S_tot, void* stream) {
+                                 int B, int S, int H, int D, int dilation, int S_tot, float scale, void* stream) {
   if (D != LH_D) return LH_ERR_UNSUPPORTED;
   if (!xq || !xk || !xv || !scores_qk || !scores_kq || dilation <= 0 || S <= 0 || S % dilation || S_tot < S)
     return LH_ERR_INVALID_ARG;
@@ -1278,7 +1278,7 @@ extern "C" int lh_dilated_scores(const void* xq, const void* xk, const void* xv,
     const void* kk = pass == 0 ? xk : xq;
     AttnArgs a{};
     int rc = fill_rows(a, qq, kk, xv, sb, ss, sh, nullptr, nullptr, nullptr, 0, 0, 0, 0, nullptr, B, VH, n, D,
-                       (float)(1.0 / 11.313708498984761));
+                       scale > 0.f ? scale : (float)(1.0 / 11.313708498984761));
     if (rc) return rc;
     a.scores = pass == 0 ? scores_qk : scores_kq;
     a.Ho = H; a.dil = dilation; a.S_tot = S_tot;

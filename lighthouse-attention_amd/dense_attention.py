@@ -33,12 +33,13 @@ def _rows(q, k, v):
 
 class _DenseCausalFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v):
+    def forward(ctx, q, k, v, scale):
         B, H, S, D = q.shape
         _mark("dense_fwd_start")
-        o, lse = N.attn_fwd(_rows(q, k, v), None, B, H, S, D)
+        o, lse = N.attn_fwd(_rows(q, k, v), None, B, H, S, D, scale)
         _mark("dense_attn_fwd")
         ctx.save_for_backward(q, k, v, o, lse)
+        ctx.scale = scale
         return o
 
     @staticmethod
@@ -49,23 +50,28 @@ class _DenseCausalFn(torch.autograd.Function):
         # softmax-backward row term delta = rowsum(dO * O), accumulated in fp32
         delta = torch.linalg.vecdot(do.float(), o.float())
         _mark("dense_bwd_start")
-        dq, dk, dv = N.attn_bwd(_rows(q, k, v), None, B, H, S, do, lse, delta, D)
+        dq, dk, dv = N.attn_bwd(_rows(q, k, v), None, B, H, S, do, lse, delta, D, ctx.scale)
         _mark("dense_attn_bwd")
-        return dq, dk, dv
+        return dq, dk, dv, None
 
 
 @graph_break
 def dense_causal_attention(q, k, v):
     """Causal softmax attention, scale 1/sqrt(D): ``q, k, v`` bf16 ``[B, H, S, D]``
-    (any batch/head/seq strides, D contiguous) -> ``[B, H, S, D]``."""
-    if q.shape[-1] != N.D_SUPPORTED:
-        raise ValueError(f"head_dim must be {N.D_SUPPORTED}, got {q.shape[-1]}")
+    (any batch/head/seq strides, D contiguous) -> ``[B, H, S, D]``.  D < 128 (a
+    multiple of 8) runs zero-padded to the kernels' 128 with scale 1/sqrt(D)."""
+    D = q.shape[-1]
+    if D > N.D_SUPPORTED or D % 8:
+        raise ValueError(f"head_dim must be a multiple of 8 and at most {N.D_SUPPORTED}, got {D}")
     if not (q.shape == k.shape == v.shape):
         raise ValueError("q, k and v must have the same shape")
     for t in (q, k, v):
         if t.dtype != torch.bfloat16:
             raise TypeError("the native attention computes in bfloat16; got " + str(t.dtype))
-    return _DenseCausalFn.apply(q, k, v)
+    if D < N.D_SUPPORTED:
+        q, k, v = (torch.nn.functional.pad(x, (0, N.D_SUPPORTED - D)) for x in (q, k, v))
+        return _DenseCausalFn.apply(q, k, v, D ** -0.5)[..., :D]
+    return _DenseCausalFn.apply(q, k, v, None)
 
 
 class ScaledDotProductAttention(nn.Module):

@@ -119,22 +119,23 @@ def _mark(name):
         _op_hook(name)
 
 
-def _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk=None):
+def _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk=None, scale=None):
     """Forward of the whole layer on contiguous bf16 [B, S, H, D] inputs:
     pyramid -> selection -> gathered causal attention -> fan-out.  The scorer is
     the norm scorer (dilation 0), the dilated one (dilation > 0) or, with the gate
     ``gk`` [B, S, H], the GLA one.  Returns ``(out, idx, saved)`` with
-    ``saved = (pq, pk, pv, inv, o, lse)``."""
+    ``saved = (pq, pk, pv, inv, o, lse)``.  ``scale``: the attention (and scorer)
+    scale, 1/sqrt(D) when None."""
     B, S, H, D = xq.shape
     _, _, S_tot = N.pyramid_lengths(S, L, p)
     _, _, _, S_sel = N.geometry(S, L, p, topk, strict)
     _mark("fwd_start")
     if gk is not None:
-        scores = N.gla_scores(xq, xk, xv, gk, dilation, S_tot)
+        scores = N.gla_scores(xq, xk, xv, gk, dilation, S_tot, scale)
         _mark("gla_scores")
         pq, pk, pv, sqk, skq = N.pyramid_fwd(xq, xk, xv, L, p, scores=scores)
     elif dilation:
-        scores = N.dilated_scores(xq, xk, xv, dilation, S_tot)
+        scores = N.dilated_scores(xq, xk, xv, dilation, S_tot, scale)
         _mark("dilated_scores")
         pq, pk, pv, sqk, skq = N.pyramid_fwd(xq, xk, xv, L, p, scores=scores)
     else:
@@ -143,22 +144,22 @@ def _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk=None
     idx, inv = N.select_topk(sqk, skq, S, L, p, topk, tie=tie, strict=strict)
     _mark("select")
     rows = _base_rows(xq, xk, xv, pq, pk, pv)
-    o, lse = N.attn_fwd(rows, idx, B, H, S_sel, D)
+    o, lse = N.attn_fwd(rows, idx, B, H, S_sel, D, scale)
     _mark("attn_fwd")
     out = N.scatter_fwd(o, inv, S, S, L, p, seq_major=seq_major)
     _mark("scatter_fwd")
     return out, idx, (pq, pk, pv, inv, o, lse)
 
 
-def _attn_bwd_pair(rows, idx, B, H, S_sel, dattn, lse, delta, D):
-    dks, dvs = N.attn_bwd_dkdv(rows, idx, B, H, S_sel, dattn, lse, delta, D)
+def _attn_bwd_pair(rows, idx, B, H, S_sel, dattn, lse, delta, D, scale=None):
+    dks, dvs = N.attn_bwd_dkdv(rows, idx, B, H, S_sel, dattn, lse, delta, D, scale)
     _mark("attn_bwd_dkdv")
-    dqs = N.attn_bwd_dq(rows, idx, B, H, S_sel, dattn, lse, delta, D)
+    dqs = N.attn_bwd_dq(rows, idx, B, H, S_sel, dattn, lse, delta, D, scale)
     _mark("attn_bwd_dq")
     return dqs, dks, dvs
 
 
-def _layer_bwd(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, L, p):
+def _layer_bwd(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, L, p, scale=None):
     """Backward of ``_layer_fwd``: fan-out adjoint (+ softmax delta) -> attention
     backward in selected space -> pyramid backward onto the base rows."""
     B, S, H, D = xq.shape
@@ -167,7 +168,7 @@ def _layer_bwd(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, L, p):
     dattn, delta = N.scatter_bwd(dout, idx, o, S, L, p)
     _mark("scatter_bwd")
     rows = _base_rows(xq, xk, xv, pq, pk, pv)
-    dqs, dks, dvs = _attn_bwd_pair(rows, idx, B, H, S_sel, dattn, lse, delta, D)
+    dqs, dks, dvs = _attn_bwd_pair(rows, idx, B, H, S_sel, dattn, lse, delta, D, scale)
     dxq, dxk, dxv = N.pyramid_bwd(dqs, dks, dvs, inv, B, S, H, L, p, D)
     _mark("pyramid_bwd")
     return dxq, dxk, dxv
@@ -177,12 +178,12 @@ class _LighthouseLayerFn(torch.autograd.Function):
     """Whole layer (``_layer_fwd`` / ``_layer_bwd``) as one autograd node."""
 
     @staticmethod
-    def forward(ctx, xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk):
+    def forward(ctx, xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk, scale):
         xq, xk, xv = xq.contiguous(), xk.contiguous(), xv.contiguous()
         out, idx, (pq, pk, pv, inv, o, lse) = _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation,
-                                                         seq_major, gk)
+                                                         seq_major, gk, scale)
         ctx.save_for_backward(xq, xk, xv, pq, pk, pv, idx, inv, o, lse)
-        ctx.geo = (L, p)
+        ctx.geo = (L, p, scale)
         ctx.mark_non_differentiable(idx)
         ctx.set_materialize_grads(False)  # no zero-filled gradient for the index output
         return out, idx
@@ -190,9 +191,9 @@ class _LighthouseLayerFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout, _didx):
         if dout is None:
-            return (None,) * 11
+            return (None,) * 12
         dx = _layer_bwd(dout, *ctx.saved_tensors, *ctx.geo)
-        return dx + (None,) * 8  # the gate gets no gradient: the scores only feed the selection
+        return dx + (None,) * 9  # the gate gets no gradient: the scores only feed the selection
 
 
 def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, topk: int = 1024,
@@ -206,9 +207,15 @@ def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, t
     stores ``out`` as ``[B, S, H, D]`` (the returned tensor is its ``[B, H, S, D]``
     view), which is the layout the model's output projection reads.  Under
     ``torch.compile`` the layer is one registered custom op (traced without a
-    graph break); eagerly it is an ``autograd.Function``; both run the same kernels."""
-    if xq.shape[-1] != N.D_SUPPORTED:
-        raise ValueError(f"head_dim must be {N.D_SUPPORTED}, got {xq.shape[-1]}")
+    graph break); eagerly it is an ``autograd.Function``; both run the same kernels.
+
+    The kernels work on 128-wide heads.  A head dim D < 128 (a multiple of 8, e.g.
+    the 64 and 72 of the patch's ablation flavors) runs zero-padded to 128 with the
+    scale 1/sqrt(D): zero columns change no dot product, norm or mean, so the
+    results are the D-wide layer's, at 128/D times the work."""
+    D = xq.shape[-1]
+    if D > N.D_SUPPORTED or D % 8:
+        raise ValueError(f"head_dim must be a multiple of 8 and at most {N.D_SUPPORTED}, got {D}")
     if not (xq.shape == xk.shape == xv.shape):
         raise AssertionError("xq, xk and xv must have the same shape (n_kv_heads == n_heads)")
     for t in (xq, xk, xv):
@@ -220,12 +227,17 @@ def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, t
         if dilation <= 0:
             raise ValueError("the GLA scorer needs dilation >= 1")
         gk = gk.detach()
+    scale = None
+    if D < N.D_SUPPORTED:
+        scale = D ** -0.5
+        xq, xk, xv = (torch.nn.functional.pad(x, (0, N.D_SUPPORTED - D)) for x in (xq, xk, xv))
     if torch.compiler.is_compiling():
         out, idx = _compiled_ops.layer_fwd(xq, xk, xv, num_levels, pooling_factor, topk, tie_break, bool(strict),
-                                           int(dilation), bool(seq_major), gk)[:2]
-        return out, idx
-    return _LighthouseLayerFn.apply(xq, xk, xv, num_levels, pooling_factor, topk, tie_break, strict,
-                                    int(dilation), bool(seq_major), gk)
+                                           int(dilation), bool(seq_major), gk, scale)[:2]
+    else:
+        out, idx = _LighthouseLayerFn.apply(xq, xk, xv, num_levels, pooling_factor, topk, tie_break, strict,
+                                            int(dilation), bool(seq_major), gk, scale)
+    return (out[..., :D] if D < N.D_SUPPORTED else out), idx
 
 
 def _rope_layer_fwd(xqkv, freqs, H, L, p, topk, tie, strict, seq_major):
@@ -343,14 +355,15 @@ class _CompiledOps:
 
         @torch.library.custom_op(f"{lib}::layer_fwd", mutates_args=(), schema=(
             "(Tensor xq, Tensor xk, Tensor xv, int L, int p, int topk, str tie, bool strict, int dilation, "
-            "bool seq_major, Tensor? gk) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)"))
-        def layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk):
+            "bool seq_major, Tensor? gk, float? scale) -> "
+            "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)"))
+        def layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk, scale):
             xq, xk, xv = xq.contiguous(), xk.contiguous(), xv.contiguous()
-            out, idx, saved = _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk)
+            out, idx, saved = _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk, scale)
             return (out, idx) + saved
 
         @layer_fwd.register_fake
-        def _(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk):
+        def _(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk, scale):
             B, S, H, D = xq.shape
             _, _, S_tot = N.pyramid_lengths(S, L, p)
             S_sel = N.geometry(S, L, p, topk, strict)[3]
@@ -362,26 +375,26 @@ class _CompiledOps:
 
         @torch.library.custom_op(f"{lib}::layer_bwd", mutates_args=(), schema=(
             "(Tensor dout, Tensor xq, Tensor xk, Tensor xv, Tensor pq, Tensor pk, Tensor pv, Tensor idx, "
-            "Tensor inv, Tensor o, Tensor lse, int L, int p) -> (Tensor, Tensor, Tensor)"))
-        def layer_bwd(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, L, p):
+            "Tensor inv, Tensor o, Tensor lse, int L, int p, float? scale) -> (Tensor, Tensor, Tensor)"))
+        def layer_bwd(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, L, p, scale):
             xq, xk, xv = xq.contiguous(), xk.contiguous(), xv.contiguous()
-            return _layer_bwd(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, L, p)
+            return _layer_bwd(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, L, p, scale)
 
         @layer_bwd.register_fake
-        def _(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, L, p):
+        def _(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, L, p, scale):
             return tuple(torch.empty(xq.shape, dtype=xq.dtype, device=xq.device) for _ in range(3))
 
         def layer_setup(ctx, inputs, output):
             xq, xk, xv, L, p = inputs[:5]
             ctx.save_for_backward(xq, xk, xv, *output[2:5], output[1], *output[5:])
-            ctx.geo = (L, p)
+            ctx.geo = (L, p, inputs[11])
 
         def layer_grad(ctx, dout, *_unused):
             if dout is None:
-                return (None,) * 11
+                return (None,) * 12
             xq, xk, xv, pq, pk, pv, idx, inv, o, lse = ctx.saved_tensors
             dx = layer_bwd(dout, xq, xk, xv, pq, pk, pv, idx, inv, o, lse, *ctx.geo)
-            return tuple(dx) + (None,) * 8
+            return tuple(dx) + (None,) * 9
 
         layer_fwd.register_autograd(layer_grad, setup_context=layer_setup)
 
@@ -435,12 +448,16 @@ _compiled_ops = _CompiledOps()
 
 class _PyramidCatFn(torch.autograd.Function):
     """The reference scorer's 5-tuple from the native pyramid; backward through the
-    dense pyramid adjoint (``g[pyramid row]`` gathered onto base rows)."""
+    dense pyramid adjoint (``g[pyramid row]`` gathered onto base rows).  Head dims
+    below 128 run zero-padded (the padded columns of the returned rows are cut off)."""
 
     @staticmethod
     def forward(ctx, xq, xk, xv, L, p, dilation, base_qk=None, base_kq=None):
-        B, S, H, D = xq.shape
+        B, S, H, D0 = xq.shape
         xq, xk, xv = xq.contiguous(), xk.contiguous(), xv.contiguous()
+        if D0 < N.D_SUPPORTED:
+            xq, xk, xv = (torch.nn.functional.pad(x, (0, N.D_SUPPORTED - D0)) for x in (xq, xk, xv))
+        D = xq.shape[-1]
         _, _, S_tot = N.pyramid_lengths(S, L, p)
         cats = [torch.empty(B, S_tot, H, D, dtype=xq.dtype, device=xq.device) for _ in range(3)]
         for c, x in zip(cats, (xq, xk, xv)):
@@ -450,24 +467,25 @@ class _PyramidCatFn(torch.autograd.Function):
             scores[0][..., :S].copy_(base_qk)
             scores[1][..., :S].copy_(base_kq)
         else:
-            scores = N.dilated_scores(xq, xk, xv, dilation, S_tot) if dilation else None
+            scores = N.dilated_scores(xq, xk, xv, dilation, S_tot, D0 ** -0.5) if dilation else None
         _, _, _, sqk, skq = N.pyramid_fwd(xq, xk, xv, L, p, scores=scores,
                                           pooled_out=tuple(c[:, S:] for c in cats))
-        ctx.geo = (B, S, H, D, L, p)
+        ctx.geo = (B, S, H, D, L, p, D0)
         ctx.mark_non_differentiable(sqk, skq)
-        return (sqk.to(xq.dtype), skq.to(xq.dtype), cats[0].transpose(1, 2), cats[1].transpose(1, 2),
-                cats[2].transpose(1, 2))
+        return (sqk.to(xq.dtype), skq.to(xq.dtype), *(c[..., :D0].transpose(1, 2) for c in cats))
 
     @staticmethod
     def backward(ctx, _g1, _g2, gq, gk, gv):
-        B, S, H, D, L, p = ctx.geo
+        B, S, H, D, L, p, D0 = ctx.geo
         gs = [g if g is not None else None for g in (gq, gk, gv)]
         ref = next((g for g in gs if g is not None), None)
         if ref is None:
             return None, None, None, None, None, None, None, None
         gs = [g.contiguous() if g is not None else torch.zeros_like(ref) for g in gs]
+        if D0 < D:
+            gs = [torch.nn.functional.pad(g, (0, D - D0)) for g in gs]
         dx = N.pyramid_bwd(*gs, None, B, S, H, L, p, D)
-        return dx[0], dx[1], dx[2], None, None, None, None, None
+        return dx[0][..., :D0], dx[1][..., :D0], dx[2][..., :D0], None, None, None, None, None
 
 
 class _GatheredAttnFn(torch.autograd.Function):
@@ -485,26 +503,35 @@ class _GatheredAttnFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q_cat, k_cat, v_cat, idx):
-        B, H, S_tot, D = q_cat.shape
+        B, H, S_tot, D0 = q_cat.shape
+        scale = None
+        if D0 < N.D_SUPPORTED:  # zero-padded head dim, scale 1/sqrt(D0)
+            q_cat, k_cat, v_cat = (torch.nn.functional.pad(x, (0, N.D_SUPPORTED - D0)) for x in (q_cat, k_cat, v_cat))
+            scale = D0 ** -0.5
+        D = q_cat.shape[-1]
         rows = _GatheredAttnFn._rows(q_cat, k_cat, v_cat)
         n = idx.shape[-1]
-        o, lse = N.attn_fwd(rows, idx, B, H, n, D)
+        o, lse = N.attn_fwd(rows, idx, B, H, n, D, scale)
         ctx.save_for_backward(q_cat, k_cat, v_cat, idx, o, lse)
-        return o
+        ctx.geo = (D0, scale)
+        return o[..., :D0] if D0 < D else o
 
     @staticmethod
     def backward(ctx, do):
         q_cat, k_cat, v_cat, idx, o, lse = ctx.saved_tensors
+        D0, scale = ctx.geo
         B, H, S_tot, D = q_cat.shape
         rows = _GatheredAttnFn._rows(q_cat, k_cat, v_cat)
         n = idx.shape[-1]
         do = do.contiguous()
+        if D0 < D:
+            do = torch.nn.functional.pad(do, (0, D - D0))
         delta = (do.float() * o.float()).sum(-1)
-        dqs, dks, dvs = N.attn_bwd(rows, idx, B, H, n, do, lse, delta, D)
+        dqs, dks, dvs = N.attn_bwd(rows, idx, B, H, n, do, lse, delta, D, scale)
         inv = N.build_inverse(idx, S_tot)
         # one-level pyramid over S_tot rows: row r receives dsel[inv[r]] (or 0)
         dq, dk, dv = N.pyramid_bwd(dqs, dks, dvs, inv, B, S_tot, H, 1, 2, D)
-        return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2), None
+        return tuple(g.transpose(1, 2)[..., :D0] for g in (dq, dk, dv)) + (None,)
 
 
 class _ScatterToBaseFn(torch.autograd.Function):
@@ -519,17 +546,22 @@ class _ScatterToBaseFn(torch.autograd.Function):
             # empty slot (skipped, as the reference's kernels skip it)
             N.check_indices(idx, -1, S_tot, unique=True, what="scatter_to_base_sequence indices")
         inv = N.build_inverse(idx, S_tot)
+        D0 = attn_out.shape[-1]
+        if D0 < N.D_SUPPORTED:  # the kernels move 128-wide rows: zero-pad, then cut the columns off
+            attn_out = torch.nn.functional.pad(attn_out, (0, N.D_SUPPORTED - D0))
         out = N.scatter_fwd(attn_out, inv, N_shard, N_total, num_levels, pooling_factor)
         ctx.save_for_backward(idx)
-        ctx.geo = (N_shard, num_levels, pooling_factor)
-        return out
+        ctx.geo = (N_shard, num_levels, pooling_factor, D0)
+        return out[..., :D0] if D0 < N.D_SUPPORTED else out
 
     @staticmethod
     def backward(ctx, grad_output):
         (idx,) = ctx.saved_tensors
-        S, L, p = ctx.geo
+        S, L, p, D0 = ctx.geo
+        if D0 < N.D_SUPPORTED:
+            grad_output = torch.nn.functional.pad(grad_output, (0, N.D_SUPPORTED - D0))
         dattn, _ = N.scatter_bwd(grad_output, idx, None, S, L, p)
-        return dattn, None, None, None, None, None, None
+        return (dattn[..., :D0] if D0 < N.D_SUPPORTED else dattn), None, None, None, None, None, None
 
 
 def scatter_to_base_sequence(attn_out, indices_hp, rank_ids_hp, N_shard: int, N_total: int,
@@ -626,8 +658,10 @@ class DilatedLighthouseGLAScorer(nn.Module):
         b, s, h, d = xq.shape
         _, _, S_tot = N.pyramid_lengths(s, self.levels, self.pooling_factor)
         with torch.no_grad():
-            sqk, skq = N.gla_scores(xq.contiguous(), xk.contiguous(), xv.contiguous(), gk.detach(), self.dilation,
-                                    S_tot, self.scaling)
+            q, k, v = (x.contiguous() for x in (xq, xk, xv))
+            if d < N.D_SUPPORTED:  # zero-padded head dim, as the native layer runs it
+                q, k, v = (torch.nn.functional.pad(x, (0, N.D_SUPPORTED - d)) for x in (q, k, v))
+            sqk, skq = N.gla_scores(q, k, v, gk.detach(), self.dilation, S_tot, self.scaling)
         return _PyramidCatFn.apply(xq, xk, xv, self.levels, self.pooling_factor, 0, sqk[..., :s], skq[..., :s])
 
 
@@ -658,7 +692,7 @@ class LighthouseLocal(nn.Module):
             return 0
         if type(sc) is DilatedLighthouseScorer and sc.attention is None:
             return sc.dilation
-        if type(sc) is DilatedLighthouseGLAScorer and sc.head_dim == N.D_SUPPORTED:  # native scale 1/sqrt(D)
+        if type(sc) is DilatedLighthouseGLAScorer:
             return sc.dilation
         return None
 

@@ -277,7 +277,7 @@ class Attention(nn.Module):
             nn.init.zeros_(self.wg.bias)
 
     def _fuses_rope(self) -> bool:
-        return (not self._needs_gate and self.n_kv_heads == self.n_heads
+        return (not self._needs_gate and self.n_kv_heads == self.n_heads and self.head_dim == 128
                 and isinstance(self.selection_attn, LighthouseLocal) and self.selection_attn.fuses_rope())
 
     def set_use_lighthouse(self, use_lighthouse: bool):

@@ -27,7 +27,7 @@ def test_layer_op_schema_and_fake(pkg, dev):
     B, S, H, D = 1, 2048, 2, 128
     g = torch.Generator(device=dev).manual_seed(0)
     xs = [torch.randn(B, S, H, D, device=dev, generator=g).bfloat16().requires_grad_() for _ in range(3)]
-    args = (*xs, 3, 4, 128, "reference", True, 0, False)
+    args = (*xs, 3, 4, 128, "reference", True, 0, False, None, None)
     torch.library.opcheck(torch.ops.lighthouse_amd.layer_fwd.default, args,
                           test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))
 
