@@ -793,6 +793,10 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
   const LaneLds ll = lane_lds(lane);
   int bh, kblk;
   schedule(blockIdx.x, a.nq, a.BH, bh, kblk, false);  // early key blocks see the most queries
+  // wave-uniform by construction; said explicitly, or the compiler keeps bh * n (and the
+  // addresses derived from it) in vector registers and spills them across the loop
+  bh = __builtin_amdgcn_readfirstlane(bh);
+  kblk = __builtin_amdgcn_readfirstlane(kblk);
   const int n = a.n;
   const BhRows m = bh_rows(a, bh);
   const int k0 = kblk * BMK, kw = k0 + 32 * pair, my_k = kw + l32;
@@ -968,7 +972,6 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
   else
     store_rows_bf16(a.dk + ((int64_t)bh * n + my_k) * LH_D, acc, a.scale, hh);
 }
-
 // ===========================================================================
 // GLA scorer: simple gated linear attention over the dilated virtual heads,
 //   o_t = scale * sum_{s <= t} exp(G_t - G_s) (q_t . k_s) v_s,  G = cumsum(g),

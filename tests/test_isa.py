@@ -39,3 +39,28 @@ def test_m0_only_in_inline_asm(tmp_path):
                 outside.append(line.strip())
     assert inside > 0, "expected the inline-asm direct loads to set M0"
     assert not outside, f"compiler-generated M0 uses: {outside[:5]}"
+
+
+SOURCES = ["lh_attn.hip", "lh_select.hip", "lh_pyramid.hip", "lh_scatter.hip", "lh_model.hip"]
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC) and shutil.which("hipcc") is None, reason="hipcc not available")
+@pytest.mark.parametrize("src", SOURCES)
+def test_no_register_spills(src, tmp_path):
+    """No kernel of the library spills registers to scratch (a spill inside the
+    attention kernels' step loops costs a memory round trip per step)."""
+    asm = _device_asm(src, tmp_path)
+    kernels, name = {}, None
+    for line in asm.split("\n"):
+        m = re.match(r"\s+\.(name|private_segment_fixed_size|vgpr_spill_count):\s+(\S+)", line)
+        if not m:
+            continue
+        if m.group(1) == "name":
+            name = m.group(2)
+            kernels[name] = [None, None]
+        elif name is not None:
+            kernels[name][0 if m.group(1) == "private_segment_fixed_size" else 1] = int(m.group(2))
+    kernels = {k: tuple(v) for k, v in kernels.items() if v[0] is not None and v[1] is not None}
+    assert kernels, "no kernel metadata found"
+    bad = {k: v for k, v in kernels.items() if v != (0, 0)}
+    assert not bad, f"kernels with scratch (private bytes, spilled VGPRs): {bad}"
