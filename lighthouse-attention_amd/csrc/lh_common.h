@@ -20,17 +20,16 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t h) {
   return __uint_as_float(((uint32_t)h) << 16);
 }
 
-// Round-to-nearest-even, NaN kept quiet.  Same rounding as torch's bf16 casts.
-__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (bf16_t)((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
+// Two fp32 -> bf16 conversions in one v_cvt_pk_bf16_f32: round to nearest even
+// (torch's bf16 cast), NaN stays NaN, no branches.
+typedef float lh_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 lh_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const lh_f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, lh_bf16x2));
 }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
-}
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) { return (bf16_t)(pack_bf16x2(f, 0.f) & 0xffffu); }
 
 // 8 bf16 held in one 16-byte register quad.
 __device__ __forceinline__ void unpack8(const uint4 v, float* f) {

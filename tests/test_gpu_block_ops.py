@@ -153,3 +153,24 @@ def test_linear_split_k_weight_grad(pkg, dev, T, O, I):
     ref_dx = dy.float() @ w.detach().float()
     assert_close(w.grad, ref_dw, "dW", max_abs=1e-2, rel_l2=4e-3)
     assert_close(x.grad, ref_dx, "dX", max_abs=1e-2, rel_l2=4e-3)
+
+
+def test_bf16_rounding_matches_torch(pkg, dev):
+    """The library's fp32 -> bf16 conversion (one v_cvt_pk_bf16_f32 per pair) is
+    torch's round-to-nearest-even, checked through lh_splitk_sum with one slice
+    (out = bf16(0 + x)) on ties of both parities, subnormals, the largest finite
+    values, overflow to infinity, infinities and random values of every scale."""
+    g = torch.Generator().manual_seed(0)
+    hi = torch.randint(0, 1 << 16, (1 << 16,), generator=g, dtype=torch.int64)
+    lo = torch.tensor([0x0000, 0x0001, 0x7fff, 0x8000, 0x8001, 0xffff], dtype=torch.int64)
+    bits = ((hi[:, None] << 16) | lo[None, :]).flatten()
+    bits = bits[((bits >> 23) & 0xff) != 0xff]  # NaN / inf patterns checked separately below
+    x = torch.cat([bits.to(torch.int32).view(torch.float32),
+                   torch.tensor([float("inf"), float("-inf"), 3.3895314e38, -3.3895314e38, 3.4e38, 1e-45, -1e-45]),
+                   torch.randn(1 << 16, generator=g) * torch.pow(2.0, torch.randint(-140, 120, (1 << 16,), generator=g))])
+    x = x[: (x.numel() // 8) * 8].contiguous()
+    got = pkg._native.splitk_sum(x[None].to(dev)).cpu()
+    want = (torch.zeros_like(x) + x).bfloat16()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    nan = pkg._native.splitk_sum(torch.full((1, 8), float("nan"), device=dev)).cpu()
+    assert torch.isnan(nan.float()).all()
