@@ -165,8 +165,9 @@ def run_gpu(args, pkg, torch):
 
     def hook(name):
         ev = torch.cuda.Event(enable_timing=True)
-        ev.record()
-        marks.append((name, ev))
+        st = torch.cuda.current_stream()
+        ev.record(st)
+        marks.append((name, ev, st.cuda_stream))
 
     sel_mod = pkg.lighthouse_selection
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -194,23 +195,36 @@ def run_gpu(args, pkg, torch):
         cfg["dilation"] = w["dilation"]
     if w.get("heavy_keys"):
         cfg["heavy_keys"] = w["heavy_keys"]
+    # the backward pair (dK/dV + dQ kernels) against the attention backward's algorithmic
+    # work, 2.5x the forward's (S, dP, dV, dK and dQ products; the dQ kernel's recomputed
+    # S and dP are not counted); with the two-stream schedule the kernels overlap, and
+    # the pair's time is the longer of the two
+    kd, kq = kernels["attn_bwd_dkdv"], kernels["attn_bwd_dq"]
+    two = sel_mod._bwd_streams >= 2
+    pair_ms = max(kd["ms"], kq["ms"]) if two else kd["ms"] + kq["ms"]
+    pair_work = kd["work"] + kq["work"]
+    pair = {"ms": round(pair_ms, 4), "algorithmic_tflop": round(pair_work / 1e12, 4),
+            "achieved": round(pair_work / (pair_ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+            "frac": round(pair_work / (pair_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "schedule": "two streams" if two else "one stream, dK/dV then dQ"}
     return {
         "tokens_per_s": tokens_per_s, "ms_step": ms_step, "wall_ms_step": wall_ms_step, "config": cfg,
-        "roofline": roofline, "kernels": kernels,
+        "roofline": roofline, "kernels": kernels, "backward_pair": pair,
     }
 
 
 def op_stats(marks, work):
-    """Per-op average launch time from (name, event) marks: each op is timed from
-    the previous mark, and a ``*_start`` mark opens a run of consecutive ops."""
+    """Per-op average launch time from (name, event, stream) marks: each op is timed
+    from the previous mark on its own stream, and a ``*_start`` mark opens a run of
+    consecutive ops on its stream (ops on a side stream are timed on that stream)."""
     per_op = {}
-    prev = None
-    for name, ev in marks:
+    prev = {}
+    for name, ev, st in marks:
         if name.endswith("_start"):
-            prev = ev
+            prev[st] = ev
             continue
-        per_op.setdefault(name, []).append(prev.elapsed_time(ev))
-        prev = ev
+        per_op.setdefault(name, []).append(prev[st].elapsed_time(ev))
+        prev[st] = ev
     kernels = {}
     for name, ts in per_op.items():
         avg_ms = sum(ts) / len(ts)
@@ -273,8 +287,9 @@ def run_model(args, pkg, torch):
 
     def hook(name):
         ev = torch.cuda.Event(enable_timing=True)
-        ev.record()
-        marks.append((name, ev))
+        st = torch.cuda.current_stream()
+        ev.record(st)
+        marks.append((name, ev, st.cuda_stream))
 
     sel_mod = pkg.lighthouse_selection
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -435,7 +450,7 @@ def main():
         "kernels": r["kernels"],
         "wall_ms_per_step": round(r["wall_ms_step"], 4),
     }
-    for key in ("native_ms_per_step", "final_loss"):
+    for key in ("backward_pair", "native_ms_per_step", "final_loss"):
         if key in r:
             line[key] = r[key]
     print(json.dumps(line))

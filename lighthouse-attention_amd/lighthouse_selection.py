@@ -39,6 +39,7 @@ Differences from the reference, all deliberate:
 from __future__ import annotations
 
 import math
+import os
 from functools import lru_cache
 
 import torch
@@ -151,11 +152,42 @@ def _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk=None
     return out, idx, (pq, pk, pv, inv, o, lse)
 
 
+# The dK/dV and dQ kernels are independent: with two streams the dQ kernel runs on a
+# side stream (default priority) beside the dK/dV kernel and fills its tail.
+_bwd_streams = int(os.environ.get("LH_BWD_STREAMS", "1"))
+_side = {}
+
+
+def set_backward_streams(n: int) -> int:
+    """1: dK/dV then dQ on the caller's stream; 2: dQ on a side stream beside dK/dV.
+    Returns the previous setting."""
+    global _bwd_streams
+    prev, _bwd_streams = _bwd_streams, int(n)
+    return prev
+
+
 def _attn_bwd_pair(rows, idx, B, H, S_sel, dattn, lse, delta, D, scale=None):
+    if _bwd_streams < 2 or torch.compiler.is_compiling():
+        dks, dvs = N.attn_bwd_dkdv(rows, idx, B, H, S_sel, dattn, lse, delta, D, scale)
+        _mark("attn_bwd_dkdv")
+        dqs = N.attn_bwd_dq(rows, idx, B, H, S_sel, dattn, lse, delta, D, scale)
+        _mark("attn_bwd_dq")
+        return dqs, dks, dvs
+    dev = dattn.device
+    main = torch.cuda.current_stream(dev)
+    side = _side.get(dev)
+    if side is None:
+        side = _side[dev] = torch.cuda.Stream(dev)
+    side.wait_stream(main)  # dattn, delta (and everything before) are ready
+    with torch.cuda.stream(side):
+        _mark("side_start")
+        dqs = N.attn_bwd_dq(rows, idx, B, H, S_sel, dattn, lse, delta, D, scale)
+        _mark("attn_bwd_dq")
     dks, dvs = N.attn_bwd_dkdv(rows, idx, B, H, S_sel, dattn, lse, delta, D, scale)
     _mark("attn_bwd_dkdv")
-    dqs = N.attn_bwd_dq(rows, idx, B, H, S_sel, dattn, lse, delta, D, scale)
-    _mark("attn_bwd_dq")
+    main.wait_stream(side)
+    dqs.record_stream(main)  # allocated on the side stream, consumed and freed on the caller's
+    _mark("join_start")
     return dqs, dks, dvs
 
 
