@@ -313,7 +313,6 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
   const int hh = lane >> 5;
   const LaneLds ll = lane_lds(lane);
   floatx16 s[2];
-  
   {
     // operand i: key block i & 1, k-slice i >> 1, so consecutive MFMAs feed
     // different accumulators; each operand is read FWD_AHEAD MFMAs early
@@ -332,7 +331,6 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
     }
     SCHED_GROUP(SG_MFMA, FWD_AHEAD);
   }
-  
   if (mask) {  // wave-uniform: only tiles that cross the diagonal or the end
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -377,7 +375,6 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
     pf[kb][0] = pack_frag(s[kb], 0);
     pf[kb][1] = pack_frag(s[kb], 1);
   }
-  
   {
     // operand i: column block i & 3 (consecutive MFMAs feed different
     // accumulators), key rows 32 (i >> 3) + 16 ((i >> 2) & 1); two transposing
@@ -395,7 +392,6 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
     }
     SCHED_GROUP(SG_MFMA, FWD_AHEAD);
   }
-  
 }
 
 template <int EPI>  // 0: O + LSE;  1: bf16-rounded row norms of O into `scores`
