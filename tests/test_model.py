@@ -144,3 +144,33 @@ def test_attention_needs_gpu(L):
     assert m.freqs_cis.is_complex()
     with pytest.raises(Exception, match="GPU|no CPU path|liblighthouse"):
         m(torch.zeros(1, 64, dtype=torch.long))
+
+
+def test_state_dict_matches_dense_flavor_and_gla_adds_the_gate(L):
+    """Checkpoint compatibility (SURVEY: the norm and dilated scorers add no
+    parameters, so a Lighthouse flavor's state dict equals its dense `_sdpa`
+    twin's, lighthouse-attention.patch:303-310; the GLA scorer adds `wg`,
+    :662-664)."""
+    def keys(**kw):
+        m = L.Transformer(_small(L, **kw))
+        return {k: tuple(v.shape) for k, v in m.state_dict().items()}
+    dense = keys(use_selection_lighthouse=False)
+    assert keys() == dense
+    assert keys(lighthouse_scorer="dilated", dilation=4) == dense
+    gla = keys(lighthouse_scorer="gla", dilation=4)
+    extra = {k: v for k, v in gla.items() if k not in dense}
+    assert {k: v for k, v in gla.items() if k in dense} == dense
+    assert extra == {f"layers.{i}.attention.wg.{n}": ((2, 256) if n == "weight" else (2,))
+                     for i in range(4) for n in ("weight", "bias")}
+
+
+def test_builder_errors_like_reference(L):
+    """_build_lighthouse_scorer's ValueErrors (lighthouse-attention.patch:610-615, 635-638)."""
+    with pytest.raises(ValueError, match="Unknown lighthouse_scorer"):
+        L.Transformer(_small(L, lighthouse_scorer="bogus"))
+    for name in ("dilated", "gla"):
+        with pytest.raises(ValueError, match="not supported under context parallelism"):
+            L.Transformer(_small(L, lighthouse_scorer=name, use_lighthouse_cp=True))
+    m = L.Transformer(_small(L, lighthouse_scorer="gla", dilation=2))
+    sc = m.layers["1"].attention.selection_attn.scorer
+    assert type(sc).__name__ == "DilatedLighthouseGLAScorer" and sc.dilation == 2 and sc.head_dim == 128

@@ -503,3 +503,48 @@ def test_gla_scorer_virtual_heads():
             assert torch.allclose(skq[:, h, r:S:dil], ok.norm(dim=-1)[..., 0].float(), rtol=1e-5, atol=1e-6)
     # pooled levels: max of the base scores over each span, as the norm scorer's
     assert torch.equal(sqk[:, :, S:S + S // 2], sqk[:, :, :S].reshape(B, H, S // 2, 2).amax(-1))
+
+
+# ----------------------------------------------------------------------------- property tests
+try:
+    from hypothesis import given, settings, strategies as st
+    HAVE_HYPOTHESIS = True
+except Exception:  # pragma: no cover
+    HAVE_HYPOTHESIS = False
+
+
+def _check_selection_properties(a, b, S, L, p, k, tie):
+    """Invariants every selection must satisfy, whatever the scores: the structural
+    and slot-literal restatements agree, and per (b, h) the indices are unique and
+    in range, and every entry below the coarsest level has its parent selected at
+    the next level."""
+    g = O.tile_geometry(S, L, p, k)
+    idx = O.select_indices(a, b, L, p, k, S, tie=tie, strict=False)
+    ref = R.select_indices_c(a, b, L, p, k, S, g.S_sel, tie=tie, strict=False)
+    assert np.array_equal(idx, ref)
+    offs = O.level_offsets(S, L, p)
+    lens = O.level_lengths(S, L, p)
+    S_tot = sum(lens)
+    for row in idx.reshape(-1, idx.shape[-1]):
+        assert len(set(row.tolist())) == len(row) and row.min() >= 0 and row.max() < S_tot
+        lvl = np.searchsorted(np.asarray(offs), row, side="right")  # 1-based level of each entry
+        loc = row - np.asarray(offs)[lvl - 1]
+        present = set(row.tolist())
+        for lv, i in zip(lvl.tolist(), loc.tolist()):
+            if lv < L:
+                parent = offs[lv] + i // p
+                if i // p < lens[lv]:
+                    assert parent in present, "an entry whose parent was not selected"
+
+
+if HAVE_HYPOTHESIS:
+    @settings(max_examples=40, deadline=None)
+    @given(L=st.integers(2, 4), p=st.sampled_from([2, 4]), kk=st.sampled_from([128, 256]),
+           mult=st.integers(1, 6), extra=st.integers(0, 37), kind=st.sampled_from(["bf16", "fp32", "coarse"]),
+           tie=st.sampled_from(["reference", "lower_index"]), seed=st.integers(0, 2 ** 31 - 1))
+    def test_selection_properties_random_geometries(L, p, kk, mult, extra, kind, tie, seed):
+        S = kk * p ** (L - 1) * mult + extra  # ragged lengths, at least one tile
+        rng = np.random.default_rng(seed)
+        a = _scores(1, 2, S, L, p, rng, kind)
+        b = _scores(1, 2, S, L, p, rng, kind)
+        _check_selection_properties(a, b, S, L, p, kk, tie)
