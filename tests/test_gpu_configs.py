@@ -31,6 +31,7 @@ CASES = [  # (workload, heads checked against the fp32 oracle)
     ("cfg3_k6144", (1,)),
     ("cfg4", (2,)),
     ("cfg5_layer", (4,)),
+    ("gla", (7,)),
 ]
 
 
@@ -41,17 +42,21 @@ def test_config_full_size(pkg, dev, name, heads):
     dil = w.get("dilation", 0)
     print(f"config {name}: S={S} L={L} p={p} k={k} scorer={w['scorer']} strict={strict} heads={heads}",
           flush=True)
-    xs, dout = bench.make_inputs(w, torch, dev)
+    xs, dout, *gate = bench.make_inputs(w, torch, dev)
+    gk = gate[0] if gate else None
     xg = [x.clone().requires_grad_() for x in xs]
     layer = bench.make_layer(w, pkg)
-    out = layer(*xg)
+    out = layer(*xg, gk=gk) if gk is not None else layer(*xg)
     out.backward(dout)
     idx = layer.last_indices
     torch.cuda.synchronize()
 
     _, _, S_tot = pkg._native.pyramid_lengths(S, L, p)
     with torch.no_grad():
-        if dil:
+        if gk is not None:
+            sc = pkg._native.gla_scores(*xs, gk, dil, S_tot)
+            _, _, _, sqk, skq = pkg._native.pyramid_fwd(*xs, L, p, scores=sc)
+        elif dil:
             sc = pkg._native.dilated_scores(*xs, dil, S_tot)
             _, _, _, sqk, skq = pkg._native.pyramid_fwd(*xs, L, p, scores=sc)
         else:
@@ -63,7 +68,12 @@ def test_config_full_size(pkg, dev, name, heads):
 
     hs = list(heads)
     xc = [x.detach().cpu()[:, :, hs].float().requires_grad_() for x in xs]
-    if dil:
+    if gk is not None:
+        r_qk, r_kq, *_ = O.gla_scorer(*[x.detach() for x in xc], gk.cpu()[:, :, hs].float(), dil, p, L,
+                                      round_bf16=True)
+        assert_close(sqk[:, hs, :S], r_qk[..., :S], f"{name} gla scores qk", max_abs=1e-2, rel_l2=5e-3)
+        assert_close(skq[:, hs, :S], r_kq[..., :S], f"{name} gla scores kq", max_abs=1e-2, rel_l2=5e-3)
+    elif dil:
         r_qk, r_kq, *_ = O.dilated_scorer(*[x.detach() for x in xc], dil, p, L)
         assert_close(sqk[:, hs, :S], r_qk[..., :S], f"{name} dilated scores qk", max_abs=1e-2, rel_l2=5e-3)
         assert_close(skq[:, hs, :S], r_kq[..., :S], f"{name} dilated scores kq", max_abs=1e-2, rel_l2=5e-3)
