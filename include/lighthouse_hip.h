@@ -124,11 +124,25 @@ int lh_dilated_scores(const void *xq, const void *xk, const void *xv,
  * DilatedLighthouseGLAScorer.forward (src/lighthouse_selection.py:713-734).
  *   xq, xk, xv  bf16 [B, S, H, D] contiguous; gk fp32 [B, S, H] contiguous log gates
  *   (token t of head h is position t / dilation of virtual head (t % dilation) * H + h)
+ *   segments   <= 0: automatic; else the number of sequence segments walked in
+ *              parallel (clamped to the 64-token chunk count).  Segment s starts
+ *              from the combined final states of segments 0..s-1, which a first
+ *              pass computes; results agree with the one-segment walk to fp32
+ *              rounding of the state (the bf16 scores may differ in the last bit).
+ *   workspace  device buffer of lh_gla_workspace_bytes(...) bytes (16-byte aligned),
+ *              may be NULL when that size is 0; workspace_bytes is its size.
  * Then lh_pyramid_fwd with base_scores_given = 1 pools the levels.
  */
 int lh_gla_scores(const void *xq, const void *xk, const void *xv, const float *gk,
                   float *scores_qk, float *scores_kq,
-                  int B, int S, int H, int D, int dilation, int S_tot, float scale, void *stream);
+                  int B, int S, int H, int D, int dilation, int S_tot, float scale,
+                  int segments, void *workspace, int64_t workspace_bytes, void *stream);
+
+/*
+ * Workspace bytes lh_gla_scores needs for this geometry and `segments` (0 when
+ * it walks one segment; -1 for an invalid geometry).  Host-only, no GPU call.
+ */
+int64_t lh_gla_workspace_bytes(int B, int S, int H, int D, int dilation, int segments);
 
 /*
  * Hierarchical per-tile top-k selection, emitted in causal order.

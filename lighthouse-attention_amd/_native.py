@@ -39,7 +39,8 @@ _SIGS = {
     "lh_pyramid_fwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _P, _P,
                             _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_dilated_scores": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P]),
-    "lh_gla_scores": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P]),
+    "lh_gla_scores": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _L, _P]),
+    "lh_gla_workspace_bytes": (_L, [_I, _I, _I, _I, _I, _I]),
     "lh_select_topk": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_build_inverse": (_I, [_P, _I, _P, _I, _I, _I, _P]),
     "lh_check_indices": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
@@ -285,9 +286,11 @@ def dilated_scores(xq, xk, xv, dilation: int, S_tot: int, scale: float | None = 
     return sqk, skq
 
 
-def gla_scores(xq, xk, xv, gk, dilation: int, S_tot: int, scale: float | None = None):
+def gla_scores(xq, xk, xv, gk, dilation: int, S_tot: int, scale: float | None = None, segments: int = 0):
     """Base-level GLA scores into fresh fp32 [B, H, S_tot] buffers (pooled levels unset).
-    ``gk`` [B, S, H] log gates (any float dtype; taken in fp32, as fla does)."""
+    ``gk`` [B, S, H] log gates (any float dtype; taken in fp32, as fla does).
+    ``segments``: sequence segments walked in parallel (0: chosen from the
+    geometry so that every CU gets a workgroup; 1: one sequential walk)."""
     _need_rows("gla_scores", xq, xk, xv)
     _need_gpu(xq, xk, xv, gk)
     B, S, H, D = xq.shape
@@ -300,9 +303,14 @@ def gla_scores(xq, xk, xv, gk, dilation: int, S_tot: int, scale: float | None = 
     sqk = torch.empty(B, H, S_tot, dtype=torch.float32, device=dev)
     skq = torch.empty_like(sqk)
     scale = D ** -0.5 if scale is None else scale
+    nbytes = lib().lh_gla_workspace_bytes(B, S, H, D, dilation, int(segments))
+    if nbytes < 0:
+        raise ValueError(f"gla_scores: invalid geometry B={B} S={S} H={H} D={D} dilation={dilation}")
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev) if nbytes else None
     with torch.cuda.device(dev):
         rc = lib().lh_gla_scores(_ptr(xq), _ptr(xk), _ptr(xv), _ptr(g), _ptr(sqk), _ptr(skq), B, S, H, D, dilation,
-                                 S_tot, float(scale), _stream(dev))
+                                 S_tot, float(scale), int(segments), _ptr(ws), nbytes,
+                                 _stream(dev))
     _check(rc, "lh_gla_scores")
     return sqk, skq
 

@@ -12,4 +12,4 @@ extern "C" const char* lh_strerror(int rc) {
   }
 }
 
-extern "C" int lh_abi_version(void) { return 4; }
+extern "C" int lh_abi_version(void) { return 5; }

@@ -36,6 +36,8 @@
 // m + log2(l) in that domain.
 #include "lh_common.h"
 
+#include <algorithm>
+
 namespace {
 
 constexpr int BMK = 128;  // keys per workgroup of the key-stationary kernel: 4 waves x 32
@@ -976,25 +978,38 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
 // chunk-local inclusive cumsum of g and H the state after the previous chunk,
 //   o = scale * ((Q K^T) o exp(b_t - b_s), causal) V + scale * exp(b_t) Q H
 //   H <- exp(b_last) H + (K o exp(b_last - b_s))^T V.
-// One workgroup (8 waves) owns one (b, virtual head, direction).  The state is
-// kept transposed, H^T [j][i] (j: value dim, i: key dim), in fp32 MFMA
-// accumulators (wave w: rows 32 (w >> 1), columns 64 (w & 1) .. + 63) with a bf16
-// copy in LDS as the operand of the inter-chunk product.  As in the forward
-// kernel, products come out transposed (A^T, O^T), so an accumulator column is
-// a token.  Per chunk: phase 1 (waves 0-2) forms the three causal 32x32 blocks
-// of A^T and hands them over in LDS as packed bf16 operands, wave 3 the decay
-// factors; phase 2 every wave forms one 32-token x 32-column block of O^T
-// (norm partials to LDS) and updates its state blocks; phase 3 writes the new
-// bf16 state copy and wave 0 finishes the norms.  Tiles of the next chunk are
-// loaded (direct global->LDS) during the current one.
+// The sequence of each (b, virtual head, direction) is cut into P segments of
+// whole chunks so that P times more workgroups share the chip.  A first pass
+// (gla_state_kernel, P - 1 segments) runs only the state recurrence of each
+// segment from a zero state and stores its final state dH_s and its decay
+// D_s = prod exp(b_last) in a workspace; the scoring pass of segment s starts
+// from H = sum_{s' < s} (prod_{s' < s'' < s} D_s'') dH_s', formed by the
+// recurrence H <- D_s' H + dH_s', and walks its own chunks.  P = 1 is the plain
+// sequential walk.
+// One workgroup (8 waves) owns one segment of one (b, virtual head,
+// direction).  The state is kept transposed, H^T [j][i] (j: value dim, i: key
+// dim), in fp32 MFMA accumulators (wave w: rows 32 (w >> 1), columns 64 (w & 1)
+// .. + 63) with a bf16 copy in LDS as the operand of the inter-chunk product.
+// As in the forward kernel, products come out transposed (A^T, O^T), so an
+// accumulator column is a token.  Per chunk: phase 1 (waves 0-2) forms the
+// three causal 32x32 blocks of A^T and hands them over in LDS as packed bf16
+// operands, wave 3 the decay factors; phase 2 every wave forms one 32-token x
+// 32-column block of O^T (norm partials to LDS) and updates its state blocks;
+// phase 3 writes the new bf16 state copy and wave 7 finishes the norms.  Tiles
+// of the next chunk are loaded (direct global->LDS) during the current one.
 // ===========================================================================
 struct GlaArgs {
   const bf16_t *q, *k, *v;  // [B, S, H, D] contiguous
   const float* g;           // [B, S, H] fp32 log gates
   float *sqk, *skq;         // [B, H, S_tot]: base level written
+  float* ws;                // P > 1: segment states [units][P - 1][8 waves][2][16][64], then decays [units][P - 1]
   int B, S, H, dil, T, S_tot;
+  int P, cps;               // segments per sequence, chunks per segment
   float scale;
 };
+
+constexpr int GLA_WS_WAVE = 2 * 16 * 64;  // fp32 state values held by one wave
+constexpr int GLA_WS_SEG = 8 * GLA_WS_WAVE;
 
 __device__ __forceinline__ void gla_issue(bf16_t* tile, const bf16_t* base, uint32_t stride, int t0, int last,
                                           int w, int lane) {
@@ -1010,6 +1025,140 @@ __device__ __forceinline__ void gla_issue(bf16_t* tile, const bf16_t* base, uint
 // bf16 element (row, col) of a swizzled 64 x 128 tile
 __device__ __forceinline__ int tile_elem(int row, int col) { return row * LH_D + ((((col >> 3) ^ swz(row)) << 3) | (col & 7)); }
 
+// The (b, virtual head, direction) sequence and segment of a workgroup:
+// blockIdx.x = (seq * nseg + seg) * 2 + dir.
+struct GlaSeq {
+  const bf16_t *qb, *kb, *vb;
+  const float* gb;
+  float* scores;
+  uint32_t stride;
+  int unit, seg, VH;
+};
+
+__device__ __forceinline__ GlaSeq gla_seq(const GlaArgs& a, int nseg) {
+  GlaSeq s;
+  s.VH = a.dil * a.H;
+  const int dir = blockIdx.x & 1;
+  const int rest = blockIdx.x >> 1;
+  const int seq = rest / nseg;
+  s.seg = rest - seq * nseg;
+  s.unit = seq * 2 + dir;
+  const int b = seq / s.VH, vh = seq % s.VH;
+  const int r = vh / a.H, ho = vh % a.H;
+  s.stride = (uint32_t)s.VH * LH_D;  // elements between consecutive tokens of a virtual head
+  const int64_t off = (int64_t)b * a.S * a.H * LH_D + (int64_t)vh * LH_D;
+  s.qb = (dir ? a.k : a.q) + off;
+  s.kb = (dir ? a.q : a.k) + off;
+  s.vb = a.v + off;
+  s.gb = a.g + (int64_t)b * a.S * a.H + vh;
+  s.scores = (dir ? a.skq : a.sqk) + ((int64_t)b * a.H + ho) * a.S_tot + r;
+  return s;
+}
+
+// chunk-local inclusive cumsum of g in log2 units (tokens past the end add 0)
+__device__ __forceinline__ float gla_cumsum(const float* G, int nvalid, int lane) {
+  float x = (lane < nvalid) ? G[lane] * 1.4426950408889634f : 0.f;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+__device__ __forceinline__ void gla_decays(float x, int nvalid, int lane, float* Es, float* Fs) {
+  const float bl = __shfl(x, nvalid - 1);
+  Es[lane] = ex2(x);
+  Fs[lane] = lane < nvalid ? ex2(bl - x) : 0.f;
+}
+
+// H^T <- exp(b_last) H^T + (V o f)^T K for this wave's two state blocks
+__device__ __forceinline__ void gla_state_update(floatx16 (&hs)[2], float el, const bf16_t* Vt, const bf16_t* Kt,
+                                                 const float* Fs, const LaneLds& ll, int sjb, int sib, int hh) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) hs[q] *= el;
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    u32x4 vt = lds_tr(Vt, ll, 16 * kk, sjb);
+    const float4 f0 = *reinterpret_cast<const float4*>(&Fs[16 * kk + 4 * hh]);
+    const float4 f1 = *reinterpret_cast<const float4*>(&Fs[16 * kk + 8 + 4 * hh]);
+    const float fv[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = __uint_as_float(vt[e] << 16) * fv[2 * e];
+      const float hi = __uint_as_float(vt[e] & 0xffff0000u) * fv[2 * e + 1];
+      vt[e] = cvt2(lo, hi);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) hs[q] = mfma(vt, lds_tr(Kt, ll, 16 * kk, sib + q), hs[q]);
+  }
+}
+
+// bf16 copy of this wave's state blocks into the LDS operand H^T
+__device__ __forceinline__ void gla_state_copy(bf16_t (*HT)[TILE], const floatx16 (&hs)[2], int sjb, int sib,
+                                               int l32, int hh) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int i = 32 * (sib + q) + l32;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int j = 32 * sjb + slot_key(v, hh);
+      HT[j >> 6][tile_elem(j & 63, i)] = (bf16_t)(cvt2(hs[q][v], 0.f) & 0xffffu);
+    }
+  }
+}
+
+// State pass: segment s < P - 1 of a sequence, from a zero state, K / V / g
+// tiles only; stores the final fp32 state blocks and the segment's decay.
+__global__ __launch_bounds__(512, 1) void gla_state_kernel(const GlaArgs a) {
+  __shared__ __attribute__((aligned(1024))) bf16_t Kt[2][TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t Vt[2][TILE];
+  __shared__ __attribute__((aligned(16))) float Gs[2][64];
+  __shared__ __attribute__((aligned(16))) float Es[64], Fs[64];
+  const int tid = threadIdx.x, lane = tid & 63, hh = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const LaneLds ll = lane_lds(lane);
+  const GlaSeq sq = gla_seq(a, a.P - 1);
+  const int T = a.T, last = T - 1;
+  const int nch = (T + 63) / 64;
+  const int c0 = sq.seg * a.cps, c1 = min(nch, c0 + a.cps);
+  const int sjb = w >> 1, sib = 2 * (w & 1);
+  floatx16 hs[2] = {floatx16{}, floatx16{}};
+  float dec = 1.f;
+
+  auto issue = [&](int c, int buf) {
+    const int t0 = 64 * c;
+    gla_issue(Kt[buf], sq.kb, sq.stride, t0, last, w, lane);
+    gla_issue(Vt[buf], sq.vb, sq.stride, t0, last, w, lane);
+    if (w == 0) g2l4(sq.gb + (int64_t)min(t0 + lane, last) * sq.VH, Gs[buf]);
+  };
+  issue(c0, 0);
+  wait_loads();
+  __syncthreads();
+  for (int c = c0; c < c1; ++c) {
+    const int buf = (c - c0) & 1;
+    const int nvalid = min(64, T - 64 * c);
+    if (c + 1 < c1) issue(c + 1, buf ^ 1);
+    if (w == 3) gla_decays(gla_cumsum(Gs[buf], nvalid, lane), nvalid, lane, Es, Fs);
+    __syncthreads();
+    const float el = Es[nvalid - 1];
+    dec *= el;
+    gla_state_update(hs, el, Vt[buf], Kt[buf], Fs, ll, sjb, sib, hh);
+    wait_loads();
+    __syncthreads();
+  }
+  float* out = a.ws + ((int64_t)(sq.unit * (a.P - 1) + sq.seg) * 8 + w) * GLA_WS_WAVE + lane;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) out[(q * 16 + v) * 64] = hs[q][v];
+  }
+  if (tid == 0) {
+    const int64_t units = (int64_t)a.B * sq.VH * 2;
+    a.ws[units * (a.P - 1) * GLA_WS_SEG + sq.unit * (a.P - 1) + sq.seg] = dec;
+  }
+}
+
 __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
   __shared__ __attribute__((aligned(1024))) bf16_t Qt[2][TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t Kt[2][TILE];
@@ -1022,56 +1171,50 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const LaneLds ll = lane_lds(lane);
-  const int VH = a.dil * a.H;
-  const int dir = blockIdx.x & 1;
-  const int seq = blockIdx.x >> 1;
-  const int b = seq / VH, vh = seq % VH;
-  const int r = vh / a.H, ho = vh % a.H;
-  const uint32_t stride = (uint32_t)VH * LH_D;  // elements between consecutive tokens of a virtual head
-  const int64_t off = (int64_t)b * a.S * a.H * LH_D + (int64_t)vh * LH_D;
-  const bf16_t* qb = (dir ? a.k : a.q) + off;
-  const bf16_t* kb = (dir ? a.q : a.k) + off;
-  const bf16_t* vb = a.v + off;
-  const float* gb = a.g + (int64_t)b * a.S * a.H + vh;
-  float* scores = (dir ? a.skq : a.sqk) + ((int64_t)b * a.H + ho) * a.S_tot + r;
+  const GlaSeq sq = gla_seq(a, a.P);
   const int T = a.T, last = T - 1;
   const int nch = (T + 63) / 64;
-  const float L2E = 1.4426950408889634f;
+  const int c0 = sq.seg * a.cps, c1 = min(nch, c0 + a.cps);
 
-  // zero state copy
-  for (int e = tid; e < 2 * TILE / 8; e += 512) reinterpret_cast<u32x4*>(&HT[0][0])[e] = u32x4{0, 0, 0, 0};
-  floatx16 hs[2] = {floatx16{}, floatx16{}};
   const int sjb = w >> 1, sib = 2 * (w & 1);  // state blocks (j block, i blocks sib, sib + 1)
   const int otb = w & 1, odb = w >> 1;         // output block (token block, column block)
+  floatx16 hs[2] = {floatx16{}, floatx16{}};
+  if (sq.seg > 0) {
+    // state entering the segment from the earlier segments' states and decays
+    const int64_t units = (int64_t)a.B * sq.VH * 2;
+    const float* dec = a.ws + units * (a.P - 1) * GLA_WS_SEG + (int64_t)sq.unit * (a.P - 1);
+    for (int s = 0; s < sq.seg; ++s) {
+      const float d = dec[s];
+      const float* in = a.ws + ((int64_t)(sq.unit * (a.P - 1) + s) * 8 + w) * GLA_WS_WAVE + lane;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) hs[q][v] = fmaf(d, hs[q][v], in[(q * 16 + v) * 64]);
+      }
+    }
+  }
+  gla_state_copy(HT, hs, sjb, sib, l32, hh);
 
   auto issue = [&](int c, int buf) {
     const int t0 = 64 * c;
-    gla_issue(Qt[buf], qb, stride, t0, last, w, lane);
-    gla_issue(Kt[buf], kb, stride, t0, last, w, lane);
-    gla_issue(Vt[buf], vb, stride, t0, last, w, lane);
-    if (w == 0) g2l4(gb + (int64_t)min(t0 + lane, last) * VH, Gs[buf]);
+    gla_issue(Qt[buf], sq.qb, sq.stride, t0, last, w, lane);
+    gla_issue(Kt[buf], sq.kb, sq.stride, t0, last, w, lane);
+    gla_issue(Vt[buf], sq.vb, sq.stride, t0, last, w, lane);
+    if (w == 0) g2l4(sq.gb + (int64_t)min(t0 + lane, last) * sq.VH, Gs[buf]);
   };
-  issue(0, 0);
+  issue(c0, 0);
   wait_loads();
   __syncthreads();
 
-  for (int c = 0; c < nch; ++c) {
-    const int buf = c & 1;
+  for (int c = c0; c < c1; ++c) {
+    const int buf = (c - c0) & 1;
     const int nvalid = min(64, T - 64 * c);
-    if (c + 1 < nch) issue(c + 1, buf ^ 1);
+    if (c + 1 < c1) issue(c + 1, buf ^ 1);
     // ---- phase 1: A^T blocks (waves 0-2), decay factors (wave 3)
     if (w < 4) {
-      // chunk-local inclusive cumsum of g (log2 units); tokens past the end add 0
-      float x = (lane < nvalid) ? Gs[buf][lane] * L2E : 0.f;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const float y = __shfl_up(x, o);
-        if (lane >= o) x += y;
-      }
+      const float x = gla_cumsum(Gs[buf], nvalid, lane);
       if (w == 3) {
-        const float bl = __shfl(x, nvalid - 1);
-        Es[lane] = ex2(x);
-        Fs[lane] = lane < nvalid ? ex2(bl - x) : 0.f;
+        gla_decays(x, nvalid, lane, Es, Fs);
       } else {
         const int tb = w == 0 ? 0 : 1, sbk = w == 2 ? 1 : 0;
         floatx16 acc = floatx16{};
@@ -1116,41 +1259,15 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
       }
       ss += __shfl_xor(ss, 32);
       if (hh == 0) RED[odb][32 * otb + l32] = ss;
-      // state: H^T <- exp(b_last) H^T + (V o f)^T K
-      const float el = Es[nvalid - 1];
-#pragma unroll
-      for (int q = 0; q < 2; ++q) hs[q] *= el;
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        u32x4 vt = lds_tr(Vt[buf], ll, 16 * kk, sjb);
-        const float4 f0 = *reinterpret_cast<const float4*>(&Fs[16 * kk + 4 * hh]);
-        const float4 f1 = *reinterpret_cast<const float4*>(&Fs[16 * kk + 8 + 4 * hh]);
-        const float fv[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float lo = __uint_as_float(vt[e] << 16) * fv[2 * e];
-          const float hi = __uint_as_float(vt[e] & 0xffff0000u) * fv[2 * e + 1];
-          vt[e] = cvt2(lo, hi);
-        }
-#pragma unroll
-        for (int q = 0; q < 2; ++q) hs[q] = mfma(vt, lds_tr(Kt[buf], ll, 16 * kk, sib + q), hs[q]);
-      }
+      gla_state_update(hs, Es[nvalid - 1], Vt[buf], Kt[buf], Fs, ll, sjb, sib, hh);
     }
     __syncthreads();
     // ---- phase 3: bf16 copy of the new state; norms of this chunk
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int i = 32 * (sib + q) + l32;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int j = 32 * sjb + slot_key(v, hh);
-        HT[j >> 6][tile_elem(j & 63, i)] = (bf16_t)(cvt2(hs[q][v], 0.f) & 0xffffu);
-      }
-    }
+    gla_state_copy(HT, hs, sjb, sib, l32, hh);
     if (w == 7 && lane < nvalid) {
       const float ss = (RED[0][lane] + RED[1][lane]) + (RED[2][lane] + RED[3][lane]);
       const uint32_t nb = cvt2(sqrtf(ss), 0.f) << 16;
-      scores[(int64_t)(64 * c + lane) * a.dil] = __uint_as_float(nb);
+      sq.scores[(int64_t)(64 * c + lane) * a.dil] = __uint_as_float(nb);
     }
     wait_loads();
     __syncthreads();
@@ -1287,22 +1404,74 @@ extern "C" int lh_dilated_scores(const void* xq, const void* xk, const void* xv,
   return LH_OK;
 }
 
-extern "C" int lh_gla_scores(const void* xq, const void* xk, const void* xv, const float* gk, float* scores_qk,
-                             float* scores_kq, int B, int S, int H, int D, int dilation, int S_tot, float scale,
-                             void* stream) {
+namespace {
+// Segments of the GLA walk: enough to give every CU a workgroup (one per CU:
+// the scoring kernel holds 139 KB of LDS), at least 8 chunks each.  segments > 0
+// asks for that many (clamped to the chunk count).  Every segment is non-empty.
+void gla_segments(int B, int S, int H, int dilation, int segments, int* P, int* cps) {
+  const int T = S / dilation;
+  const int nch = (T + 63) / 64;
+  const long long units = (long long)B * dilation * H * 2;
+  long long want = segments;
+  if (want <= 0) {
+    want = units >= 256 ? 1 : 256 / units;
+    want = std::min<long long>(want, std::max(1, nch / 8));
+  }
+  want = std::max<long long>(1, std::min<long long>(want, nch));
+  *cps = (int)((nch + want - 1) / want);
+  *P = (nch + *cps - 1) / *cps;
+}
+
+int gla_check(const void* xq, const void* xk, const void* xv, const float* gk, int B, int S, int H, int D,
+              int dilation, float scale) {
   if (D != LH_D) return LH_ERR_UNSUPPORTED;
-  if (!xq || !xk || !xv || !gk || !scores_qk || !scores_kq || B <= 0 || H <= 0 || dilation <= 0 || S <= 0 ||
-      S % dilation || S_tot < S || !(scale > 0.f))
+  if (!xq || !xk || !xv || !gk || B <= 0 || H <= 0 || dilation <= 0 || S <= 0 || S % dilation || !(scale > 0.f))
     return LH_ERR_INVALID_ARG;
   if (!al16(xq) || !al16(xk) || !al16(xv) || (reinterpret_cast<uintptr_t>(gk) & 3u)) return LH_ERR_INVALID_ARG;
   // token offsets inside one virtual head are 32-bit
-  if ((long long)S * H * D > 0x7fffffffLL || (long long)B * dilation * H * 2 > 0x7fffffffLL) return LH_ERR_UNSUPPORTED;
+  if ((long long)S * H * D > 0x7fffffffLL || (long long)B * dilation * H * 2 > 0x7fffffffLL)
+    return LH_ERR_UNSUPPORTED;
+  return LH_OK;
+}
+
+long long gla_ws_bytes(int B, int H, int dilation, int P) {
+  if (P <= 1) return 0;
+  const long long units = (long long)B * dilation * H * 2;
+  return units * (P - 1) * ((long long)GLA_WS_SEG + 1) * (long long)sizeof(float);
+}
+}  // namespace
+
+extern "C" int64_t lh_gla_workspace_bytes(int B, int S, int H, int D, int dilation, int segments) {
+  if (B <= 0 || H <= 0 || dilation <= 0 || S <= 0 || S % dilation || D != LH_D) return -1;
+  int P, cps;
+  gla_segments(B, S, H, dilation, segments, &P, &cps);
+  return gla_ws_bytes(B, H, dilation, P);
+}
+
+extern "C" int lh_gla_scores(const void* xq, const void* xk, const void* xv, const float* gk, float* scores_qk,
+                             float* scores_kq, int B, int S, int H, int D, int dilation, int S_tot, float scale,
+                             int segments, void* workspace, int64_t workspace_bytes, void* stream) {
+  int rc = gla_check(xq, xk, xv, gk, B, S, H, D, dilation, scale);
+  if (rc) return rc;
+  if (!scores_qk || !scores_kq || S_tot < S) return LH_ERR_INVALID_ARG;
   GlaArgs a{};
   a.q = (const bf16_t*)xq; a.k = (const bf16_t*)xk; a.v = (const bf16_t*)xv; a.g = gk;
   a.sqk = scores_qk; a.skq = scores_kq;
   a.B = B; a.S = S; a.H = H; a.dil = dilation; a.T = S / dilation; a.S_tot = S_tot; a.scale = scale;
-  hipLaunchKernelGGL(gla_scores_kernel, dim3(B * dilation * H * 2), dim3(512), 0,
-                     reinterpret_cast<hipStream_t>(stream), a);
+  gla_segments(B, S, H, dilation, segments, &a.P, &a.cps);
+  const long long units = (long long)B * dilation * H * 2;
+  if (units * a.P > 0x7fffffffLL) return LH_ERR_UNSUPPORTED;
+  if (a.P > 1) {
+    if (!workspace || !al16(workspace) || workspace_bytes < gla_ws_bytes(B, H, dilation, a.P))
+      return LH_ERR_INVALID_ARG;
+    a.ws = (float*)workspace;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (a.P > 1) {
+    hipLaunchKernelGGL(gla_state_kernel, dim3((unsigned)(units * (a.P - 1))), dim3(512), 0, st, a);
+    LH_CHECK_LAUNCH();
+  }
+  hipLaunchKernelGGL(gla_scores_kernel, dim3((unsigned)(units * a.P)), dim3(512), 0, st, a);
   LH_CHECK_LAUNCH();
   return LH_OK;
 }

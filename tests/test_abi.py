@@ -37,7 +37,24 @@ def test_library_exports_every_declared_symbol(pkg):
     for n in _declared():
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
     assert set(_declared()) == set(pkg._native.EXPORTED)
-    assert lib.lh_abi_version() == 4
+    assert lib.lh_abi_version() == 5
+
+
+def test_gla_workspace_geometry(pkg):
+    """Host-only size query of the segmented GLA walk: one segment needs no
+    workspace; otherwise (P - 1) fp32 128 x 128 states plus one decay per
+    (b, virtual head, direction); invalid geometry gives -1."""
+    f = pkg._native.lib().lh_gla_workspace_bytes
+    units = 1 * 4 * 8 * 2  # cfg2 with dilation 4: B * dilation * H * 2
+    assert f(1, 32768, 8, 128, 4, 0) == units * 3 * (128 * 128 + 1) * 4  # 4 segments of 32 chunks
+    assert f(1, 32768, 8, 128, 4, 1) == 0
+    assert f(1, 32768, 8, 128, 4, 6) == units * 5 * (128 * 128 + 1) * 4  # 128 chunks: 22 per segment, 6 segments
+    assert f(1, 32768, 8, 128, 4, 100000) == units * 127 * (128 * 128 + 1) * 4  # clamped to one chunk each
+    assert f(1, 1024, 2, 128, 4, 0) == 0  # 4 chunks: fewer than 8 per segment, one walk
+    assert f(64, 32768, 8, 128, 4, 0) == 0  # 4096 workgroups already
+    assert f(1, 1000, 1, 128, 3, 0) == -1  # S not a multiple of the dilation
+    assert f(1, 1024, 1, 64, 4, 0) == -1  # D != 128
+    assert f(0, 1024, 1, 128, 4, 0) == -1
 
 
 def test_strerror(pkg):

@@ -115,3 +115,52 @@ def test_gla_model_layer(pkg, dev):
     assert torch.isfinite(loss)
     assert att.wg.weight.grad is None
     assert att.wq.weight.grad is not None and torch.isfinite(att.wq.weight.grad.float()).all()
+
+
+@pytest.mark.parametrize("B,S,H,dil,gate,segs", [(1, 8192, 1, 2, "typical", (2, 3, 5, 0, 64)),
+                                                 (1, 1000, 2, 4, "strong", (2, 3, 4)),
+                                                 (2, 4096, 1, 1, "none", (3, 0, 64))])
+def test_gla_segments(pkg, dev, B, S, H, dil, gate, segs):
+    """The segmented walk (a first pass forms each segment's final state from a zero
+    state; segment s starts from the decayed sum of the earlier ones) against the
+    oracle and against the one-segment walk on the same inputs, including a last
+    chunk shorter than 64 tokens and one chunk per segment."""
+    N = pkg._native
+    L, p = 3, 2
+    xs, gk, xd, gd = _inputs(B, S, H, gate, 7 * S + H, dev)
+    _, _, S_tot = N.pyramid_lengths(S, L, p)
+    r_qk, r_kq, *_ = O.gla_scorer(*[x.float() for x in xs], gk.float(), dil, p, L, round_bf16=True)
+    one = N.gla_scores(*xd, gd, dil, S_tot, segments=1)
+    assert N.lib().lh_gla_workspace_bytes(B, S, H, D, dil, 1) == 0
+    for segments in segs:
+        print(f"gla segments={segments} B={B} S={S} H={H} dil={dil} gate={gate}", flush=True)
+        assert N.lib().lh_gla_workspace_bytes(B, S, H, D, dil, segments) > 0 or segments == 0
+        got = N.gla_scores(*xd, gd, dil, S_tot, segments=segments)
+        for g_, o_, ref, name in zip(got, one, (r_qk, r_kq), ("qk", "kq")):
+            g_ = g_[..., :S].cpu()
+            o_ = o_[..., :S].cpu()
+            assert_close(g_, ref[..., :S], f"gla segments={segments} {name}")
+            assert (_ulps(g_, ref[..., :S]) <= 1).float().mean().item() >= 0.95
+            # against the sequential walk: the state differs only by fp32 rounding
+            u = _ulps(g_, o_)
+            assert u.max().item() <= 2, f"segments={segments} {name}: {u.max().item()} ulps from one segment"
+            assert (u == 0).float().mean().item() >= 0.97, f"segments={segments} {name}: too many differ"
+
+
+def test_gla_workspace_errors(pkg, dev):
+    """A missing or short workspace is rejected before any launch."""
+    N = pkg._native
+    lib = N.lib()
+    B, S, H, dil = 1, 8192, 1, 2
+    xs, gk, xd, gd = _inputs(B, S, H, "typical", 3, dev)
+    need = lib.lh_gla_workspace_bytes(B, S, H, D, dil, 4)
+    assert need > 0
+    out = [torch.empty(B, H, S, device=dev) for _ in range(2)]
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    ptr = N._ptr
+    args = [ptr(xd[0]), ptr(xd[1]), ptr(xd[2]), ptr(gd.float().contiguous()), ptr(out[0]), ptr(out[1]),
+            B, S, H, D, dil, S, 1.0 / D ** 0.5, 4]
+    assert lib.lh_gla_scores(*args, None, 0, N._stream(dev)) == 1  # LH_ERR_INVALID_ARG
+    assert lib.lh_gla_scores(*args, ptr(ws), need - 4, N._stream(dev)) == 1  # LH_ERR_INVALID_ARG
+    assert lib.lh_gla_scores(*args, ptr(ws), need, N._stream(dev)) == 0
+    torch.cuda.synchronize()
