@@ -1055,19 +1055,31 @@ __device__ __forceinline__ GlaSeq gla_seq(const GlaArgs& a, int nseg) {
   return s;
 }
 
-// chunk-local inclusive cumsum of g in log2 units (tokens past the end add 0)
+template <int CTRL>
+__device__ __forceinline__ float dpp0(float x) {  // DPP move, 0 where the source lane is outside the row
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_value(float x, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+
+// Chunk-local inclusive cumsum of g in log2 units (tokens past the end add 0):
+// Hillis-Steele within each 16-lane row by DPP row shifts, then the row totals
+// carried across rows.
 __device__ __forceinline__ float gla_cumsum(const float* G, int nvalid, int lane) {
   float x = (lane < nvalid) ? G[lane] * 1.4426950408889634f : 0.f;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const float y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  return x;
+  x += dpp0<0x111>(x);  // row_shr:1
+  x += dpp0<0x112>(x);  // row_shr:2
+  x += dpp0<0x114>(x);  // row_shr:4
+  x += dpp0<0x118>(x);  // row_shr:8
+  const float r0 = lane_value(x, 15), r1 = lane_value(x, 31), r2 = lane_value(x, 47);
+  const int row = lane >> 4;
+  const float r01 = r0 + r1;
+  return x + (row == 0 ? 0.f : row == 1 ? r0 : row == 2 ? r01 : r01 + r2);
 }
 
 __device__ __forceinline__ void gla_decays(float x, int nvalid, int lane, float* Es, float* Fs) {
-  const float bl = __shfl(x, nvalid - 1);
+  const float bl = lane_value(x, nvalid - 1);
   Es[lane] = ex2(x);
   Fs[lane] = lane < nvalid ? ex2(bl - x) : 0.f;
 }
@@ -1110,11 +1122,13 @@ __device__ __forceinline__ void gla_state_copy(bf16_t (*HT)[TILE], const floatx1
 
 // State pass: segment s < P - 1 of a sequence, from a zero state, K / V / g
 // tiles only; stores the final fp32 state blocks and the segment's decay.
+// Every wave forms the chunk's decay factors itself (in a wave-private LDS
+// row), so one barrier per chunk (tile reuse) suffices.
 __global__ __launch_bounds__(512, 1) void gla_state_kernel(const GlaArgs a) {
   __shared__ __attribute__((aligned(1024))) bf16_t Kt[2][TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t Vt[2][TILE];
   __shared__ __attribute__((aligned(16))) float Gs[2][64];
-  __shared__ __attribute__((aligned(16))) float Es[64], Fs[64];
+  __shared__ __attribute__((aligned(16))) float Fw[8][64];  // wave w's exp(b_last - b_s)
   const int tid = threadIdx.x, lane = tid & 63, hh = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const LaneLds ll = lane_lds(lane);
@@ -1139,11 +1153,12 @@ __global__ __launch_bounds__(512, 1) void gla_state_kernel(const GlaArgs a) {
     const int buf = (c - c0) & 1;
     const int nvalid = min(64, T - 64 * c);
     if (c + 1 < c1) issue(c + 1, buf ^ 1);
-    if (w == 3) gla_decays(gla_cumsum(Gs[buf], nvalid, lane), nvalid, lane, Es, Fs);
-    __syncthreads();
-    const float el = Es[nvalid - 1];
+    const float x = gla_cumsum(Gs[buf], nvalid, lane);
+    const float bl = lane_value(x, nvalid - 1);
+    Fw[w][lane] = lane < nvalid ? ex2(bl - x) : 0.f;
+    const float el = ex2(bl);
     dec *= el;
-    gla_state_update(hs, el, Vt[buf], Kt[buf], Fs, ll, sjb, sib, hh);
+    gla_state_update(hs, el, Vt[buf], Kt[buf], Fw[w], ll, sjb, sib, hh);
     wait_loads();
     __syncthreads();
   }
@@ -1159,15 +1174,25 @@ __global__ __launch_bounds__(512, 1) void gla_state_kernel(const GlaArgs a) {
   }
 }
 
+// Scoring pass.  Per chunk c two phases, each closed by a barrier:
+//   A: every wave forms its O^T block (inter-chunk H^T Q^T + intra-chunk
+//      V^T A^T), its norm partials, and updates its state blocks;
+//   B: the new bf16 state copy; wave 7 finishes chunk c's norms; waves 0-2
+//      form the A^T blocks of chunk c + 1 and wave 3 its decay factors (both
+//      double-buffered), so that phase A of the next chunk starts at once.
+// Tiles of chunk c + 2 are issued at the start of phase B of chunk c, into the
+// buffers chunk c has just released, and waited for at the end of phase A of
+// chunk c + 1.
 __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
   __shared__ __attribute__((aligned(1024))) bf16_t Qt[2][TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t Kt[2][TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t Vt[2][TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t HT[2][TILE];  // bf16 H^T: rows j, columns i
   __shared__ __attribute__((aligned(16))) float Gs[2][64];
-  __shared__ __attribute__((aligned(16))) float Es[64], Fs[64];  // exp(b_t), exp(b_last - b_s) (0 past the end)
-  __shared__ u32x4 AP[3][2][64];                                  // packed A^T blocks (s0,t0), (s0,t1), (s1,t1)
-  __shared__ float RED[4][64];                                    // norm partials per column block
+  __shared__ __attribute__((aligned(16))) float Es[2][64], Fs[2][64];  // exp(b_t), exp(b_last - b_s) (0 past the end)
+  __shared__ __attribute__((aligned(16))) float Bw[3][64];             // b of waves 0-2 (wave-private rows)
+  __shared__ u32x4 AP[2][3][2][64];  // packed A^T blocks (s0,t0), (s0,t1), (s1,t1) per buffer
+  __shared__ float RED[4][64];       // norm partials per column block
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const LaneLds ll = lane_lds(lane);
@@ -1202,39 +1227,48 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
     gla_issue(Vt[buf], sq.vb, sq.stride, t0, last, w, lane);
     if (w == 0) g2l4(sq.gb + (int64_t)min(t0 + lane, last) * sq.VH, Gs[buf]);
   };
+  // A^T blocks (waves 0-2) and decay factors (wave 3) of chunk c from buffer buf
+  auto prep = [&](int c, int buf) {
+    if (w >= 4) return;
+    const int nvalid = min(64, T - 64 * c);
+    const float x = gla_cumsum(Gs[buf], nvalid, lane);
+    if (w == 3) {
+      gla_decays(x, nvalid, lane, Es[buf], Fs[buf]);
+      return;
+    }
+    Bw[w][lane] = x;  // read back below by this wave only (LDS keeps a wave's order)
+    const int tb = w == 0 ? 0 : 1, sbk = w == 2 ? 1 : 0;
+    floatx16 acc = floatx16{};
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) acc = mfma(lds_row(Kt[buf], ll, sbk, cc), lds_row(Qt[buf], ll, tb, cc), acc);
+    const int t = 32 * tb + l32;
+    const float bt = Bw[w][t];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int s0 = 32 * sbk + 8 * g + 4 * hh;  // slots v = 4 g .. 4 g + 3 hold keys s0 .. s0 + 3
+      const float4 bs = *reinterpret_cast<const float4*>(&Bw[w][s0]);
+      const float b4[4] = {bs.x, bs.y, bs.z, bs.w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int v = 4 * g + r, s = s0 + r;
+        acc[v] = (s <= t && s < nvalid) ? acc[v] * a.scale * ex2(bt - b4[r]) : 0.f;
+      }
+    }
+    AP[buf][w][0][lane] = pack_frag(acc, 0);
+    AP[buf][w][1][lane] = pack_frag(acc, 1);
+  };
+
   issue(c0, 0);
   wait_loads();
+  __syncthreads();
+  if (c0 + 1 < c1) issue(c0 + 1, 1);
+  prep(c0, 0);
   __syncthreads();
 
   for (int c = c0; c < c1; ++c) {
     const int buf = (c - c0) & 1;
     const int nvalid = min(64, T - 64 * c);
-    if (c + 1 < c1) issue(c + 1, buf ^ 1);
-    // ---- phase 1: A^T blocks (waves 0-2), decay factors (wave 3)
-    if (w < 4) {
-      const float x = gla_cumsum(Gs[buf], nvalid, lane);
-      if (w == 3) {
-        gla_decays(x, nvalid, lane, Es, Fs);
-      } else {
-        const int tb = w == 0 ? 0 : 1, sbk = w == 2 ? 1 : 0;
-        floatx16 acc = floatx16{};
-#pragma unroll
-        for (int cc = 0; cc < 8; ++cc)
-          acc = mfma(lds_row(Kt[buf], ll, sbk, cc), lds_row(Qt[buf], ll, tb, cc), acc);
-        const int t = 32 * tb + l32;
-        const float bt = __shfl(x, t);
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int s = 32 * sbk + slot_key(v, hh);
-          const float bs = __shfl(x, s);
-          acc[v] = (s <= t && s < nvalid) ? acc[v] * a.scale * ex2(bt - bs) : 0.f;
-        }
-        AP[w][0][lane] = pack_frag(acc, 0);
-        AP[w][1][lane] = pack_frag(acc, 1);
-      }
-    }
-    __syncthreads();
-    // ---- phase 2: O^T block (otb, odb) and the state update
+    // ---- phase A: O^T block (otb, odb), norm partials, state update
     {
       floatx16 oi = floatx16{}, oa = floatx16{};
       // inter-chunk: H^T rows of column block odb against the chunk's queries
@@ -1247,9 +1281,10 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
         if (sbk > otb) break;
         const int blk = otb == 0 ? 0 : 1 + sbk;
 #pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2) oa = mfma(lds_tr(Vt[buf], ll, 32 * sbk + 16 * c2, odb), AP[blk][c2][lane], oa);
+        for (int c2 = 0; c2 < 2; ++c2)
+          oa = mfma(lds_tr(Vt[buf], ll, 32 * sbk + 16 * c2, odb), AP[buf][blk][c2][lane], oa);
       }
-      const float et = Es[32 * otb + l32] * a.scale;
+      const float et = Es[buf][32 * otb + l32] * a.scale;
       float ss = 0.f;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
@@ -1259,17 +1294,19 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
       }
       ss += __shfl_xor(ss, 32);
       if (hh == 0) RED[odb][32 * otb + l32] = ss;
-      gla_state_update(hs, Es[nvalid - 1], Vt[buf], Kt[buf], Fs, ll, sjb, sib, hh);
+      gla_state_update(hs, Es[buf][nvalid - 1], Vt[buf], Kt[buf], Fs[buf], ll, sjb, sib, hh);
     }
+    wait_loads();  // tiles of chunk c + 1
     __syncthreads();
-    // ---- phase 3: bf16 copy of the new state; norms of this chunk
+    // ---- phase B: bf16 copy of the new state; norms of chunk c; A^T and decays of chunk c + 1
+    if (c + 2 < c1) issue(c + 2, buf);
     gla_state_copy(HT, hs, sjb, sib, l32, hh);
     if (w == 7 && lane < nvalid) {
       const float ss = (RED[0][lane] + RED[1][lane]) + (RED[2][lane] + RED[3][lane]);
       const uint32_t nb = cvt2(sqrtf(ss), 0.f) << 16;
       sq.scores[(int64_t)(64 * c + lane) * a.dil] = __uint_as_float(nb);
     }
-    wait_loads();
+    if (c + 1 < c1) prep(c + 1, buf ^ 1);
     __syncthreads();
   }
 }
