@@ -1026,7 +1026,9 @@ __device__ __forceinline__ void gla_issue(bf16_t* tile, const bf16_t* base, uint
 __device__ __forceinline__ int tile_elem(int row, int col) { return row * LH_D + ((((col >> 3) ^ swz(row)) << 3) | (col & 7)); }
 
 // The (b, virtual head, direction) sequence and segment of a workgroup:
-// blockIdx.x = (seq * nseg + seg) * 2 + dir.
+// logical block (seq * nseg + seg) * 2 + dir, taken through xcd_block so that
+// the two directions of a segment, which stream the same q, k and v rows in
+// step, run on one XCD and share its L2.
 struct GlaSeq {
   const bf16_t *qb, *kb, *vb;
   const float* gb;
@@ -1038,8 +1040,9 @@ struct GlaSeq {
 __device__ __forceinline__ GlaSeq gla_seq(const GlaArgs& a, int nseg) {
   GlaSeq s;
   s.VH = a.dil * a.H;
-  const int dir = blockIdx.x & 1;
-  const int rest = blockIdx.x >> 1;
+  const int blk = (int)xcd_block(blockIdx.x, gridDim.x);
+  const int dir = blk & 1;
+  const int rest = blk >> 1;
   const int seq = rest / nseg;
   s.seg = rest - seq * nseg;
   s.unit = seq * 2 + dir;
