@@ -73,14 +73,18 @@ __device__ __forceinline__ void cx_lane(float& s, int& x, int& id, bool desc, in
   const int oid = TIE ? lane_xor<J>(id, lane) : 0;
   const int j = J;
   const bool keep_max = (((lane & j) == 0) == desc);
+  // take = keep_max ? (s < os) : (s > os), as one compare of a lane-ordered
+  // pair (a, b) = keep_max ? (s, os) : (os, s): take = a < b
+  const float a = keep_max ? s : os, b = keep_max ? os : s;
   bool take;
   if (TIE == LH_TIE_REFERENCE) {
-    take = keep_max ? (s < os) : (s > os);
+    take = a < b;
   } else {
-    const unsigned mk = (unsigned)id, ok = (unsigned)oid;  // -1 -> largest: invalid ids lose ties
-    const bool other_better = (os > s) || (os == s && ok < mk);
-    const bool mine_better = (s > os) || (s == os && mk < ok);
-    take = keep_max ? other_better : mine_better;
+    // other_better on keep_max lanes, mine_better elsewhere: b beats a on the
+    // score, or ties with a smaller id (-1 -> largest: invalid ids lose ties)
+    const unsigned mk = (unsigned)id, ok = (unsigned)oid;
+    const unsigned ai = keep_max ? mk : ok, bi = keep_max ? ok : mk;
+    take = (b > a) || (b == a && bi < ai);
   }
   if (take) { s = os; x = ox; id = oid; }
 }
