@@ -497,8 +497,11 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], const u32x4 (&qf)[8]
       u32x4 f[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) f[i] = lds_row((i & 1) ? Vs : Ks, ll, kb, i >> 1);
+      floatx16 dinit;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) dinit[v] = -dlt;  // the accumulator ends as dP - delta
       s = mfma(f[0], qf[0], floatx16{});
-      dp = mfma(f[1], df[0], floatx16{});
+      dp = mfma(f[1], df[0], dinit);
 #pragma unroll
       for (int i = 2; i < 16; i += 2) {
         s = mfma(f[i], qf[i >> 1], s);
@@ -521,7 +524,7 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], const u32x4 (&qf)[8]
       }
     }
 #pragma unroll
-    for (int v = 0; v < 16; ++v) s[v] = ex2(fmaf(s[v], sl2, nlse)) * (dp[v] - dlt);
+    for (int v = 0; v < 16; ++v) s[v] = ex2(fmaf(s[v], sl2, nlse)) * dp[v];
     const u32x4 f0 = pack_frag(s, 0), f1 = pack_frag(s, 1);
     __builtin_amdgcn_s_setprio(1);
     {
