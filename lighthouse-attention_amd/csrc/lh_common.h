@@ -56,6 +56,19 @@ __device__ __forceinline__ long long xcd_block(long long w, long long total) {
   return (total & 7) ? w : (w & 7) * (total >> 3) + (w >> 3);
 }
 
+// Runs of `run` consecutive blocks per XCD, the XCDs taking turns: dispatch
+// index w (XCD w % 8) -> logical block, a bijection on [0, total) (the
+// incomplete last group of 8 runs keeps the dispatch order).  Neighbouring
+// blocks still share an L2, while every XCD sees the whole index range, so
+// work that varies along it stays balanced across XCDs.
+__device__ __forceinline__ long long xcd_run(long long w, long long total, int run) {
+  const long long span = 8LL * run;
+  const long long g = w / span;
+  if ((g + 1) * span > total) return w;
+  const long long r = w - g * span;
+  return g * span + (r & 7) * run + (r >> 3);
+}
+
 // ---------------------------------------------------------------------------
 // Rotary embedding of 8 consecutive elements of a row (pairs j = 0..3 are
 // (f[2j], f[2j+1])) by the angles whose (cos, sin) pairs are c01 = (c0, s0, c1, s1)

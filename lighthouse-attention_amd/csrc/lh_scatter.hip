@@ -28,11 +28,14 @@ struct ScatArgs {
 
 __device__ __forceinline__ uint4 ld16(const bf16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
-// Both kernels take their block index through xcd_block: consecutive blocks
+// Both kernels take their block index through xcd_run: consecutive blocks
 // share rows (neighbouring base tokens read the same selected rows; a node's
 // span overlaps its descendants', which precede it in causal order), and
 // workgroups are dispatched round-robin over the 8 XCDs, each with its own L2,
-// so runs of consecutive blocks are kept on one XCD.
+// so runs of SCAT_RUN consecutive blocks are kept on one XCD.  Short runs
+// rather than one contiguous eighth per XCD: an eighth is one head here, and the
+// span lengths (the adjoint's work) differ from head to head.
+constexpr int SCAT_RUN = 16;
 //
 // Forward: each 16-lane group owns SF_ROWS output rows (16 apart); all their
 // levels' inverse lookups are issued first, then all row loads, so a group
@@ -42,7 +45,7 @@ template <int NL, int R>
 __global__ __launch_bounds__(256) void scatter_fwd_kernel(const ScatArgs a) {
   const int tid = threadIdx.x;
   const int l16 = tid & 15;
-  const long long row0 = xcd_block(blockIdx.x, gridDim.x) * (16 * R) + (tid >> 4);
+  const long long row0 = xcd_run(blockIdx.x, gridDim.x, SCAT_RUN) * (16 * R) + (tid >> 4);
   int s[R][NL], tr[R];
   long long bhr[R];
 #pragma unroll
@@ -89,7 +92,7 @@ __global__ __launch_bounds__(256) void scatter_fwd_kernel(const ScatArgs a) {
 // loads), and the attention-output row for delta is loaded up front.
 __global__ __launch_bounds__(256) void scatter_bwd_kernel(const ScatArgs a) {
   const int tid = threadIdx.x;
-  const long long row = xcd_block(blockIdx.x, gridDim.x) * 16 + (tid >> 4);
+  const long long row = xcd_run(blockIdx.x, gridDim.x, SCAT_RUN) * 16 + (tid >> 4);
   const int l16 = tid & 15;
   if (row >= a.rows) return;  // all 16 lanes of a row leave together
   const long long bh = row / a.n;
