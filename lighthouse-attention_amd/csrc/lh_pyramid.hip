@@ -186,8 +186,10 @@ struct PyrBwdArgs {
 // One 16-lane group per (b, t, h) row, 8 d each; a block covers 16 consecutive
 // tokens of one (b, h), so the rows of a pooled node spanning up to 16 tokens
 // are read by one block (the wave or block coalesces the repeats instead of
-// several blocks fetching the row through L2), and consecutive chunks of a head
-// stay on one XCD (`xcd_block`).  All levels' inverse lookups
+// several blocks fetching the row through L2), and runs of 32 consecutive
+// chunks of a head stay on one XCD (`xcd_run`; one whole head per XCD left the
+// XCDs unevenly loaded, as the gathered rows per token differ by head).  All
+// levels' inverse lookups
 // are issued first, then all gradient-row loads, so a row costs two dependent
 // memory round trips instead of two per level.  ROPE: the q and k sums are
 // the gradients of rotated rows; they are rotated back (the adjoint of the
@@ -195,7 +197,7 @@ struct PyrBwdArgs {
 template <int NL, bool ROPE>
 __global__ __launch_bounds__(256) void pyramid_bwd_kernel(const PyrBwdArgs a) {
   const int tid = threadIdx.x;
-  const long long blk = xcd_block(blockIdx.x, gridDim.x);
+  const long long blk = xcd_run(blockIdx.x, gridDim.x, 32);
   const long long bh = blk / a.chunks;
   const int t = (int)(blk - bh * a.chunks) * 16 + (tid >> 4);
   const int l16 = tid & 15;
