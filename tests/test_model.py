@@ -147,7 +147,7 @@ def test_attention_needs_gpu(L):
 
 
 def test_state_dict_matches_dense_flavor_and_gla_adds_the_gate(L):
-    """Checkpoint compatibility (SURVEY: the norm and dilated scorers add no
+    """Checkpoint compatibility (the norm and dilated scorers add no
     parameters, so a Lighthouse flavor's state dict equals its dense `_sdpa`
     twin's, lighthouse-attention.patch:303-310; the GLA scorer adds `wg`,
     :662-664)."""

@@ -32,7 +32,8 @@ from oracle import select_ref as R
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
-# BASELINE.md size table: (S, L, p, k) -> (S_sel by the reference formula, S_sel generalized)
+# Selected lengths of the benchmark geometries: (S, L, p, k) -> (S_sel by the reference formula,
+# src/lighthouse_selection_cuda.py:346-357, S_sel generalized)
 TABLE = {
     (4096, 3, 4, 1536): (12544, 5292),
     (32768, 3, 4, 2048): (18432, 18432),
