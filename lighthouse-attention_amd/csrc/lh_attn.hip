@@ -37,6 +37,10 @@
 #include "lh_common.h"
 
 #include <algorithm>
+#include <atomic>
+#include <map>
+#include <mutex>
+#include <vector>
 
 namespace {
 
@@ -129,6 +133,40 @@ __device__ __forceinline__ void schedule(int w, int nblk, int BH, int& bh, int& 
   bh = t / nblk;
   const int r = t % nblk;
   blk = heavy_last ? (nblk - 1 - r) : r;
+}
+
+// Query-block plan of the query-stationary kernels.  Causal query blocks of one
+// (b, h) cost 1, 2, .. nq key tiles, and with one (b, h) per XCD the hardware's
+// heaviest-first list scheduling leaves about 8% of the XCD's CUs idle at the
+// end (72 blocks on 32 CUs at cfg2).  With a plan the grid is one workgroup
+// per CU: workgroup w (XCD w % 8) is bin (w / 8) % bph of (b, h)
+// 8 ((w / 8) / bph) + w % 8 and runs, one after the other, the query blocks
+// blk[bin * ipb + k] (k < ipb, PLAN_NONE = none), packed on the host so that
+// every bin carries nearly the same number of key tiles.  bph = 0: no plan,
+// one query block per workgroup (`schedule`).  The plan travels in the kernel
+// arguments: no device state, so concurrent launches cannot interfere.
+constexpr int QPLAN_MAX = 1024;
+constexpr uint16_t PLAN_NONE = 0xffff;
+struct QPlan {
+  int bph;  // bins (workgroups) per (b, h); 0 = no plan
+  int ipb;  // slots per bin
+  uint16_t blk[QPLAN_MAX];
+};
+
+// (b, h), first query block (without a plan) and number of blocks of this workgroup
+__device__ __forceinline__ void plan_slot(const QPlan& p, int w, int nq, int BH, int& bh, int& bin, int& nitems,
+                                          int& qb0) {
+  if (p.bph == 0) {
+    schedule(w, nq, BH, bh, qb0, true);
+    bin = 0;
+    nitems = 1;
+  } else {
+    const int i = w >> 3;
+    bh = (i / p.bph) * 8 + (w & 7);
+    bin = i % p.bph;
+    nitems = p.ipb;
+    qb0 = 0;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -396,17 +434,13 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
   }
 }
 
+// One query block qb of (b, h) bh.
 template <int EPI>  // 0: O + LSE;  1: bf16-rounded row norms of O into `scores`
-__global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArgs a) {
+__device__ __forceinline__ void fwd_block(const AttnArgs& a, int bh, int qb, bf16_t* K0, bf16_t* K1, bf16_t* V0,
+                                          bf16_t* V1) {
   constexpr int BM = 32 * QW;
-  __shared__ __attribute__((aligned(1024))) bf16_t K0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t K1[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t V0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t V1[TILE];
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  int bh, qb;
-  schedule(blockIdx.x, a.nq, a.BH, bh, qb, true);
   const int n = a.n;
   const BhRows m = bh_rows(a, bh);
   const int q0 = qb * BM, qw = q0 + wave * 32, my_q = qw + l32;
@@ -479,6 +513,27 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArg
   }
 }
 
+template <int EPI>
+__global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArgs a, const QPlan p) {
+  __shared__ __attribute__((aligned(1024))) bf16_t K0[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t K1[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t V0[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t V1[TILE];
+  int bh, bin, nitems, qb;
+  plan_slot(p, blockIdx.x, a.nq, a.BH, bh, bin, nitems, qb);
+  for (int k = 0; k < nitems; ++k) {
+    if (p.bph) {
+      qb = p.blk[bin * p.ipb + k];
+      if (qb == PLAN_NONE) break;
+    }
+    if (k) {  // the previous block's loads have landed and its last tile reads are done
+      wait_loads();
+      __syncthreads();
+    }
+    fwd_block<EPI>(a, bh, qb, K0, K1, V0, V1);
+  }
+}
+
 // ===========================================================================
 // backward dQ (query-stationary)
 // ===========================================================================
@@ -546,16 +601,12 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], const u32x4 (&qf)[8]
   }
 }
 
-__global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const AttnArgs a) {
+// dQ of one query block qb of (b, h) bh.
+__device__ __forceinline__ void dq_block(const AttnArgs& a, int bh, int qb, bf16_t* K0, bf16_t* K1, bf16_t* V0,
+                                         bf16_t* V1) {
   constexpr int BM = 32 * QW;
-  __shared__ __attribute__((aligned(1024))) bf16_t K0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t K1[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t V0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t V1[TILE];
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  int bh, qb;
-  schedule(blockIdx.x, a.nq, a.BH, bh, qb, true);
   const int n = a.n;
   const BhRows m = bh_rows(a, bh);
   const int q0 = qb * BM, qw = q0 + wave * 32, my_q = qw + l32;
@@ -605,6 +656,26 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const Attn
 
   if (my_q >= n) return;
   store_rows_bf16(a.dq + ((int64_t)bh * n + my_q) * LH_D, acc, a.scale, hh);
+}
+
+__global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const AttnArgs a, const QPlan p) {
+  __shared__ __attribute__((aligned(1024))) bf16_t K0[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t K1[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t V0[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t V1[TILE];
+  int bh, bin, nitems, qb;
+  plan_slot(p, blockIdx.x, a.nq, a.BH, bh, bin, nitems, qb);
+  for (int k = 0; k < nitems; ++k) {
+    if (p.bph) {
+      qb = p.blk[bin * p.ipb + k];
+      if (qb == PLAN_NONE) break;
+    }
+    if (k) {  // the previous block's loads have landed and its last tile reads are done
+      wait_loads();
+      __syncthreads();
+    }
+    dq_block(a, bh, qb, K0, K1, V0, V1);
+  }
 }
 
 // ===========================================================================
@@ -973,6 +1044,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a)
   else
     store_rows_bf16(a.dk + ((int64_t)bh * n + my_k) * LH_D, acc, a.scale, hh);
 }
+
 // ===========================================================================
 // GLA scorer: simple gated linear attention over the dilated virtual heads,
 //   o_t = scale * sum_{s <= t} exp(G_t - G_s) (q_t . k_s) v_s,  G = cumsum(g),
@@ -1347,6 +1419,104 @@ int fill_rows(AttnArgs& a, const void* q, const void* k, const void* v, int64_t 
   return LH_OK;
 }
 
+// CUs of the current device (cached per device); 0 when unknown.
+int cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int c = cache[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = -1;
+    cache[dev].store(c, std::memory_order_relaxed);
+  }
+  return c > 0 ? c : 0;
+}
+
+// Best-fit-decreasing packing of costs w into at most nb bins of capacity cap:
+// each block, heaviest first, goes to the fullest bin it still fits in.
+bool pack_bfd(const std::vector<int>& w, const std::vector<int>& order, int nb, long long cap,
+              std::vector<std::vector<int>>& bins) {
+  bins.assign(nb, {});
+  std::vector<long long> load(nb, 0);
+  int used = 0;
+  for (int b : order) {
+    int best = -1;
+    for (int j = 0; j < used; ++j)
+      if (load[j] + w[b] <= cap && (best < 0 || load[j] > load[best])) best = j;
+    if (best < 0) {
+      if (used == nb) return false;
+      best = used++;
+    }
+    bins[best].push_back(b);
+    load[best] += w[b];
+  }
+  return true;
+}
+
+// Query-block plan of a query-stationary launch over BH (b, h) of length n:
+// bph = CUs / BH bins per (b, h), each (b, h)'s bins on one XCD.  A block of
+// 32 QW queries costs its key tiles (counted in half tiles) plus about 1.5
+// tiles of set-up and stores; the blocks are packed best-fit-decreasing into
+// bph bins of the smallest capacity (binary search from the larger of the
+// heaviest block and the mean) for which they fit.  No plan (one block per
+// workgroup) when the bins would not fill whole XCDs or every block has a CU
+// of its own anyway.  Plans are cached per geometry.  Returns the grid size.
+int make_plan(int BH, int n, QPlan& p) {
+  p.bph = 0;
+  p.ipb = 0;
+  const int nb = (n + 32 * QW - 1) / (32 * QW);
+  const int plain = nb * BH;
+  const int cus = cu_count();
+  if (cus <= 0 || cus % 8 || BH % 8 || BH > cus || (cus / 8) % (BH / 8)) return plain;
+  const int bph = cus / BH;
+  if (nb <= bph || nb >= (int)PLAN_NONE) return plain;
+  const long long key = ((long long)cus << 48) | ((long long)BH << 32) | (long long)n;
+  static std::mutex mu;
+  static std::map<long long, QPlan> cache;
+  {
+    std::lock_guard<std::mutex> g(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) {
+      p = it->second;
+      return p.bph ? p.bph * BH : plain;
+    }
+  }
+  std::vector<int> w(nb), order(nb);
+  long long total = 0;
+  for (int b = 0; b < nb; ++b) {
+    w[b] = 2 * ((std::min((b + 1) * 32 * QW, n) + BN - 1) / BN) + 3;
+    order[b] = b;
+    total += w[b];
+  }
+  std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return w[x] > w[y]; });
+  std::vector<std::vector<int>> bins, best;
+  long long lo = std::max<long long>(w[order[0]], (total + bph - 1) / bph), hi = total;
+  while (lo < hi) {  // smallest capacity the packing fits in (it always fits at the total)
+    const long long mid = (lo + hi) / 2;
+    if (pack_bfd(w, order, bph, mid, bins)) {
+      best = bins;
+      hi = mid;
+    } else {
+      lo = mid + 1;
+    }
+  }
+  if (best.empty() || !pack_bfd(w, order, bph, lo, best)) pack_bfd(w, order, bph, total, best);
+  int ipb = 0;
+  for (auto& bn : best) ipb = std::max(ipb, (int)bn.size());
+  if ((long long)ipb * bph <= QPLAN_MAX) {
+    for (int j = 0; j < bph; ++j) {
+      std::stable_sort(best[j].begin(), best[j].end(), [&](int x, int y) { return w[x] > w[y]; });
+      for (int k = 0; k < ipb; ++k) p.blk[j * ipb + k] = k < (int)best[j].size() ? (uint16_t)best[j][k] : PLAN_NONE;
+    }
+    p.bph = bph;
+    p.ipb = ipb;
+  }
+  std::lock_guard<std::mutex> g(mu);
+  if (cache.size() >= 256) cache.clear();
+  cache[key] = p;
+  return p.bph ? p.bph * BH : plain;
+}
+
 }  // namespace
 
 extern "C" int lh_attn_fwd(const void* q, const void* k, const void* v, int64_t sb, int64_t ss, int64_t sh,
@@ -1358,8 +1528,9 @@ extern "C" int lh_attn_fwd(const void* q, const void* k, const void* v, int64_t 
   if (rc) return rc;
   if (!out || !lse || !al16(out)) return LH_ERR_INVALID_ARG;
   a.out = (bf16_t*)out; a.lse = lse;
-  hipLaunchKernelGGL(attn_fwd_kernel<0>, dim3(a.nq * a.BH), dim3(64 * QW), 0, reinterpret_cast<hipStream_t>(stream),
-                     a);
+  QPlan p;
+  const int grid = make_plan(a.BH, a.n, p);
+  hipLaunchKernelGGL(attn_fwd_kernel<0>, dim3(grid), dim3(64 * QW), 0, reinterpret_cast<hipStream_t>(stream), a, p);
   LH_CHECK_LAUNCH();
   return LH_OK;
 }
@@ -1390,7 +1561,9 @@ int attn_bwd_parts(int parts, const void* q, const void* k, const void* v, int64
     LH_CHECK_LAUNCH();
   }
   if (parts & 2) {
-    hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3(a.nq * a.BH), dim3(64 * QW), 0, st, a);
+    QPlan p;
+    const int grid = make_plan(a.BH, a.n, p);
+    hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3(grid), dim3(64 * QW), 0, st, a, p);
     LH_CHECK_LAUNCH();
   }
   return LH_OK;
@@ -1441,7 +1614,9 @@ extern "C" int lh_dilated_scores(const void* xq, const void* xk, const void* xv,
     if (rc) return rc;
     a.scores = pass == 0 ? scores_qk : scores_kq;
     a.Ho = H; a.dil = dilation; a.S_tot = S_tot;
-    hipLaunchKernelGGL(attn_fwd_kernel<1>, dim3(a.nq * a.BH), dim3(64 * QW), 0, st, a);
+    QPlan p;
+    const int grid = make_plan(a.BH, a.n, p);
+    hipLaunchKernelGGL(attn_fwd_kernel<1>, dim3(grid), dim3(64 * QW), 0, st, a, p);
     LH_CHECK_LAUNCH();
   }
   return LH_OK;
