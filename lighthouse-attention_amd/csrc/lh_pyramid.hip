@@ -244,9 +244,9 @@ __global__ __launch_bounds__(256) void pyramid_bwd_kernel(const PyrBwdArgs a) {
     rope_rotate8<false>(fk, c01, c23);
   }
   const int64_t o = (int64_t)b * a.ob + (int64_t)t * a.os + (int64_t)h * a.oh + 8 * l16;
-  if (a.dq) *reinterpret_cast<uint4*>(a.dq + o) = pack8(fq);
-  if (a.dk) *reinterpret_cast<uint4*>(a.dk + o) = pack8(fk);
-  if (a.dv) *reinterpret_cast<uint4*>(a.dv + o) = pack8(fv);
+  if (a.dq) store16_nt(a.dq + o, pack8(fq));
+  if (a.dk) store16_nt(a.dk + o, pack8(fk));
+  if (a.dv) store16_nt(a.dv + o, pack8(fv));
 }
 
 template <int NL>

@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void scatter_fwd_kernel(const ScatArgs a) {
       for (int e = 0; e < 8; ++e) acc[e] += f[e];
     }
     const int b = (int)(bhr[r] / a.H), h = (int)(bhr[r] % a.H);
-    *reinterpret_cast<uint4*>(a.dst + b * a.sb + h * a.sh + (int64_t)tr[r] * a.st + 8 * l16) = pack8(acc);
+    store16_nt(a.dst + b * a.sb + h * a.sh + (int64_t)tr[r] * a.st + 8 * l16, pack8(acc));
   }
 }
 
