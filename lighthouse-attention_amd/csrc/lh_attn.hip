@@ -741,12 +741,14 @@ __device__ __forceinline__ void rows16_lds(int (&r)[4], const int* ix, int w, in
   for (int i = 0; i < 4; ++i) r[i] = ix[16 * w + 4 * i + (lane >> 4)];
 }
 
-// Issue order of an MFMA phase built as: 16 transposing reads (8 operands),
-// 16 more, their 8 + 8 MFMAs, 8 + 8 row reads, their 8 + 8 MFMAs.  Each
-// operand group is read while the previous group's MFMAs run, so LDS latency
-// overlaps the matrix core and at most two operand groups are live.
+// Issue order of an MFMA phase built as: the NINIT accumulator-start reads,
+// 16 transposing reads (8 operands), 16 more, their 8 + 8 MFMAs, 8 + 8 row
+// reads, their 8 + 8 MFMAs.  Each operand group is read while the previous
+// group's MFMAs run, so LDS latency overlaps the matrix core and at most two
+// operand groups are live.
+template <int NINIT>
 __device__ __forceinline__ void mma_phase_order() {
-  SCHED_GROUP(SG_DSR, 24);  // the 8 accumulator-init reads, then the first 8 operands
+  SCHED_GROUP(SG_DSR, NINIT + 16);  // the accumulator-start reads, then the first 8 operands
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     SCHED_GROUP(SG_DSR, 2);
@@ -765,6 +767,31 @@ __device__ __forceinline__ void mma_phase_order() {
   SCHED_GROUP(SG_MFMA, 8);
 }
 
+// S accumulator start of a 32-query block for the P waves: slot 4 g + i of
+// lane (hh, j) holds query 8 g + 4 hh + i (g, i < 4) and starts from
+// lse[query] * nisl2.  Each lane reads one float4 (group g = lane % 4), and
+// quad broadcasts (DPP quad_perm [g, g, g, g], fused into the multiply) give it
+// the other three groups: 1 KB of LDS reads per wave instead of 4 KB of float4s
+// that the 32 lanes of a half share.  (The dS waves keep the plain reads: their
+// start values need no multiply, and 32 separate DPP moves cost more than the
+// reads they save.)
+template <int G>
+__device__ __forceinline__ float quad_bcast(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), G * 0x55, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ void s_start(floatx16& a, const float* lse, float nisl2) {
+  const int lane = __lane_id();
+  const float4 x = *reinterpret_cast<const float4*>(lse + 8 * (lane & 3) + 4 * (lane >> 5));
+#define LH_QB(G)                            \
+  a[4 * G + 0] = quad_bcast<G>(x.x) * nisl2; \
+  a[4 * G + 1] = quad_bcast<G>(x.y) * nisl2; \
+  a[4 * G + 2] = quad_bcast<G>(x.z) * nisl2; \
+  a[4 * G + 3] = quad_bcast<G>(x.w) * nisl2;
+  LH_QB(0) LH_QB(1) LH_QB(2) LH_QB(3)
+#undef LH_QB
+}
+
 // MFMA phase of a P wave: dV += dO^T P of the previous tile (Dp, pp), then
 // S of the current tile (Qc).  Operands are read a group ahead of their MFMAs.
 __device__ __forceinline__ void pw_mma(floatx16 (&s)[2], floatx16 (&dva)[4], const u32x4 (&kf)[8],
@@ -772,19 +799,8 @@ __device__ __forceinline__ void pw_mma(floatx16 (&s)[2], floatx16 (&dva)[4], con
                                        const LaneLds& ll, const float* lse, float nisl2) {
   // S starts from -lse / (scale log2 e) of its query, so that P = exp2(S scale log2 e)
   floatx16 si[2];
-  {
-    const int hh = __lane_id() >> 5;
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float4 l4 = *reinterpret_cast<const float4*>(lse + qb * 32 + 8 * g + 4 * hh);
-        si[qb][4 * g + 0] = l4.x * nisl2;
-        si[qb][4 * g + 1] = l4.y * nisl2;
-        si[qb][4 * g + 2] = l4.z * nisl2;
-        si[qb][4 * g + 3] = l4.w * nisl2;
-      }
-  }
+  s_start(si[0], lse, nisl2);
+  s_start(si[1], lse + 32, nisl2);
   u32x4 oa[8], ob[8], ka[8], kb[8];
   // operand i: rows 32 qb + 16 c2 with qb = i & 1, c2 = (i >> 1) & 1; column block db = i >> 2 (+2)
 #pragma unroll
@@ -806,7 +822,7 @@ __device__ __forceinline__ void pw_mma(floatx16 (&s)[2], floatx16 (&dva)[4], con
 #pragma unroll
   for (int c = 1; c < 8; ++c) s[1] = mfma(kb[c], kf[c], s[1]);
 
-  mma_phase_order();
+  mma_phase_order<2>();
 }
 
 // MFMA phase of a dS wave: dK += Q^T dS of the previous tile (Qp, dsf), then
@@ -849,7 +865,7 @@ __device__ __forceinline__ void dw_mma(floatx16 (&dp)[2], floatx16 (&dka)[4], co
 #pragma unroll
   for (int c = 1; c < 8; ++c) dp[1] = mfma(kb[c], vf[c], dp[1]);
 
-  mma_phase_order();
+  mma_phase_order<8>();
 }
 
 template <bool GATHER>
