@@ -119,6 +119,14 @@ __device__ __forceinline__ uint32_t cvt2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
+// two packed bf16 as the vector type of the dot builtins (a memcpy: this
+// compiler mis-lowers __builtin_bit_cast of a single vector element)
+__device__ __forceinline__ bf16x2 as_bf2(uint32_t u) {
+  bf16x2 r;
+  __builtin_memcpy(&r, &u, 4);
+  return r;
+}
+
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ u32x4 ldg16(const bf16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
@@ -398,22 +406,33 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
     st.m = m_new;
   }
   const float nm = (st.m == -INFINITY) ? 0.f : -st.m * sl2;
-  float ls = 0.f;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const float p = ex2(fmaf(s[kb][v], sl2, nm));
-      s[kb][v] = p;
-      ls += p;
-    }
+    for (int v = 0; v < 16; ++v) s[kb][v] = ex2(fmaf(s[kb][v], sl2, nm));
   }
-  st.l += ls;
   u32x4 pf[2][2];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     pf[kb][0] = pack_frag(s[kb], 0);
     pf[kb][1] = pack_frag(s[kb], 1);
+  }
+  // Row sum of the bf16 P that the P V product uses, two terms per v_dot2
+  // (16 instructions instead of 32 adds); the weights of O then sum to 1
+  // exactly, up to the fp32 accumulation.
+  {
+    const bf16x2 one = as_bf2(0x3f803f80u);
+    float ls = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        ls = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(pf[kb][h].x), one, ls, false);
+        ls = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(pf[kb][h].y), one, ls, false);
+        ls = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(pf[kb][h].z), one, ls, false);
+        ls = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(pf[kb][h].w), one, ls, false);
+      }
+    st.l += ls;
   }
   {
     // operand i: column block i & 3 (consecutive MFMAs feed different
