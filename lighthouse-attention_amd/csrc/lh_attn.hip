@@ -49,7 +49,7 @@ constexpr int QW = 8;     // waves per workgroup of the query-stationary kernels
 constexpr int BN = 64;   // rows per LDS tile
 constexpr float RESCALE_LOG2 = 8.0f;
 constexpr int FWD_AHEAD = 4;  // forward: LDS operands read this many MFMAs ahead
-constexpr int DQ_AHEAD = 8;   // dQ kernel, S and dP products
+constexpr int DQ_AHEAD = 4;   // dQ kernel, S and dP products
 constexpr int DQ_AHEAD2 = 4;  // dQ kernel, dS K product
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
