@@ -193,7 +193,9 @@ int lh_check_indices(const int32_t *indices, int B, int H, int n, int lo, int hi
  * Precondition (not checked on the device): 0 <= indices[b,h,s] < split + P,
  * P the number of pooled rows behind `pool` (S_tot - S for a pyramid); the
  * kernels read row r unguarded.  lh_check_indices validates an index array.
- *   out  bf16 [B, H, n, D];  lse fp32 [B, H, n] (log2-domain: m*log2(e)+log2(sum))
+ *   out  bf16 [B, H, n, D];  lse fp32 [B, H, n] (log2-domain: m*log2(e)+log2(sum),
+ *        sum = the row sum of the bf16-rounded probabilities that weight V, so
+ *        the weights of each output row sum to 1 up to fp32 accumulation)
  */
 int lh_attn_fwd(const void *q, const void *k, const void *v, int64_t sb, int64_t ss, int64_t sh,
                 const void *qp, const void *kp, const void *vp, int64_t pb, int64_t ps, int64_t ph,
