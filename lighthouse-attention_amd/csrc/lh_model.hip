@@ -127,6 +127,21 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const bf16_t* __restri
 // Block = 4 waves over a contiguous range of rows; each block leaves one fp32
 // partial of every dw column (stored column-major, [dim][blocks]) for
 // rmsnorm_dw_kernel.
+// one row's dy, x and (if given) dres slices of this lane
+template <int NC>
+__device__ __forceinline__ void rms_bwd_load(const bf16_t* __restrict__ dy, const bf16_t* __restrict__ x,
+                                             const bf16_t* __restrict__ dres, int64_t row, int dim, int lane,
+                                             uint4 (&a)[NC], uint4 (&b)[NC], uint4 (&c2)[NC]) {
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int col = (c * 64 + lane) * kVec;
+    a[c] = col < dim ? ld16(dy + row * dim + col) : zero;
+    b[c] = col < dim ? ld16(x + row * dim + col) : zero;
+    c2[c] = (dres && col < dim) ? ld16(dres + row * dim + col) : zero;
+  }
+}
+
 template <int NC>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const bf16_t* __restrict__ dy, const bf16_t* __restrict__ x,
                                                           const bf16_t* __restrict__ w, const float* __restrict__ rstd,
@@ -147,14 +162,20 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const bf16_t* __restri
 #pragma unroll
     for (int e = 0; e < kVec; ++e) acc[c][e] = 0.f;
   }
+  // Each wave walks every fourth row of the block; the next row's dy, x (and
+  // dres) are loaded before this row's reduction, so a row's memory latency
+  // overlaps the previous row's work.
+  uint4 cd[NC], cx[NC], cr[NC];
+  if (r0 + wave < r1) rms_bwd_load<NC>(dy, x, dres, r0 + wave, dim, lane, cd, cx, cr);
   for (int64_t row = r0 + wave; row < r1; row += 4) {
     float g[NC][kVec], xv[NC][kVec], d[NC][kVec];
+    uint4 nd[NC], nx[NC], nr[NC];
+    if (row + 4 < r1) rms_bwd_load<NC>(dy, x, dres, row + 4, dim, lane, nd, nx, nr);
     float dot = 0.f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int col = (c * 64 + lane) * kVec;
-      unpack8(col < dim ? ld16(dy + row * dim + col) : zero, d[c]);
-      unpack8(col < dim ? ld16(x + row * dim + col) : zero, xv[c]);
+      unpack8(cd[c], d[c]);
+      unpack8(cx[c], xv[c]);
 #pragma unroll
       for (int e = 0; e < kVec; ++e) {
         g[c][e] = d[c][e] * wf[c][e];
@@ -175,12 +196,18 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const bf16_t* __restri
       if (col < dim) {
         if (dres) {  // gradient arriving through the residual branch, summed before one rounding
           float rv[kVec];
-          unpack8(ld16(dres + row * dim + col), rv);
+          unpack8(cr[c], rv);
 #pragma unroll
           for (int e = 0; e < kVec; ++e) g[c][e] += rv[e];
         }
         st16(dx + row * dim + col, pack8(g[c]));
       }
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      cd[c] = nd[c];
+      cx[c] = nx[c];
+      cr[c] = nr[c];
     }
   }
   // reduce the four waves' dw partials through LDS, NC chunks at a time in halves
