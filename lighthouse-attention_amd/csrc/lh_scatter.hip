@@ -89,10 +89,14 @@ __global__ __launch_bounds__(256) void scatter_fwd_kernel(const ScatArgs a) {
 }
 
 // Backward: the span's dout rows are loaded eight at a time (independent
-// loads), and the attention-output row for delta is loaded up front.
-__global__ __launch_bounds__(256) void scatter_bwd_kernel(const ScatArgs a) {
+// loads), and the attention-output row for delta is loaded up front.  A block
+// is one wave (4 rows; spans of 1 to p^(L-1) rows make waves finish at
+// different times, and one-wave blocks free their slots soonest); XCD runs
+// stay 256 rows long.
+constexpr int SB_ROWS = 4;
+__global__ __launch_bounds__(16 * SB_ROWS) void scatter_bwd_kernel(const ScatArgs a) {
   const int tid = threadIdx.x;
-  const long long row = xcd_run(blockIdx.x, gridDim.x, SCAT_RUN) * 16 + (tid >> 4);
+  const long long row = xcd_run(blockIdx.x, gridDim.x, SCAT_RUN * 16 / SB_ROWS) * SB_ROWS + (tid >> 4);
   const int l16 = tid & 15;
   if (row >= a.rows) return;  // all 16 lanes of a row leave together
   const long long bh = row / a.n;
@@ -192,9 +196,10 @@ extern "C" int lh_scatter_bwd(const void* dout, int64_t db, int64_t dh, int64_t 
   a.src = (const bf16_t*)dout; a.map = indices; a.o = (const bf16_t*)o; a.dst = (bf16_t*)dattn; a.delta = delta;
   a.rows = (long long)B * H * n;
   if (a.rows == 0) return LH_OK;
-  const long long blocks = (a.rows + 15) / 16;
+  const long long blocks = (a.rows + SB_ROWS - 1) / SB_ROWS;
   if (blocks > 2147483647LL) return LH_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(scatter_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), a);
+  hipLaunchKernelGGL(scatter_bwd_kernel, dim3((unsigned)blocks), dim3(16 * SB_ROWS), 0,
+                     reinterpret_cast<hipStream_t>(stream), a);
   LH_CHECK_LAUNCH();
   return LH_OK;
 }
