@@ -153,7 +153,9 @@ def _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk=None
 
 
 # The dK/dV and dQ kernels are independent: with two streams the dQ kernel runs on a
-# side stream (default priority) beside the dK/dV kernel and fills its tail.
+# side stream (default priority) beside the dK/dV kernel.  One stream is the default:
+# the dQ kernel's query-block plan assumes the whole GPU, and beside the dK/dV kernel
+# the pair measured slower than one after the other.
 _bwd_streams = int(os.environ.get("LH_BWD_STREAMS", "1"))
 _side = {}
 

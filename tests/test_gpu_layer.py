@@ -98,3 +98,24 @@ def test_local_module_api(pkg, dev):
     out2.backward(dout.to(dev))
     for n, g1, x in zip("qkv", grads, xs2):
         assert_close(x.grad, g1.float(), f"generic path d{n}", max_abs=1e-2, rel_l2=4e-3)
+
+
+def test_layer_backward_two_streams(pkg, dev):
+    """set_backward_streams(2) runs the dQ kernel on a side stream beside the
+    dK/dV kernel: the same kernels on the same inputs, so the gradients must be
+    bit-equal to the one-stream order."""
+    S, H, L, p, k = 4096, 8, 3, 4, 256
+    cpu, _, dout = _inputs(1, S, H, 11, dev)
+    grads = []
+    for streams in (1, 2):
+        prev = pkg.lighthouse_selection.set_backward_streams(streams)
+        try:
+            xs = [c.to(dev).requires_grad_() for c in cpu]
+            out, _ = pkg.lighthouse_layer(*xs, num_levels=L, pooling_factor=p, topk=k)
+            out.backward(dout.to(dev))
+            torch.cuda.synchronize()
+            grads.append([x.grad.clone() for x in xs])
+        finally:
+            pkg.lighthouse_selection.set_backward_streams(prev)
+    for n, g1, g2 in zip("qkv", *grads):
+        assert torch.equal(g1, g2), f"d{n} differs between one and two backward streams"
