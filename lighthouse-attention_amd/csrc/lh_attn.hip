@@ -40,6 +40,8 @@
 #include <atomic>
 #include <map>
 #include <mutex>
+#include <thread>
+#include <utility>
 #include <vector>
 
 namespace {
@@ -150,8 +152,8 @@ __device__ __forceinline__ void schedule(int w, int nblk, int BH, int& bh, int& 
 // per CU: workgroup w (XCD w % 8) is bin (w / 8) % bph of (b, h)
 // 8 ((w / 8) / bph) + w % 8 and runs, one after the other, the query blocks
 // blk[bin * ipb + k] (k < ipb, PLAN_NONE = none), packed on the host so that
-// every bin carries nearly the same number of key tiles.  bph = 0: no plan,
-// one query block per workgroup (`schedule`).  The plan travels in the kernel
+// every bin carries nearly the same number of key tiles.  bph = 0: no plan
+// (work queues or one block per workgroup).  The plan travels in the kernel
 // arguments: no device state, so concurrent launches cannot interfere.  Plans
 // are used only up to 3.5 blocks per bin: with more blocks per CU the list
 // schedule is already balanced, and the packed bins measured slower (dense
@@ -164,20 +166,109 @@ struct QPlan {
   uint16_t blk[QPLAN_MAX];
 };
 
-// (b, h), first query block (without a plan) and number of blocks of this workgroup
-__device__ __forceinline__ void plan_slot(const QPlan& p, int w, int nq, int BH, int& bh, int& bin, int& nitems,
-                                          int& qb0) {
-  if (p.bph == 0) {
-    schedule(w, nq, BH, bh, qb0, true);
-    bin = 0;
-    nitems = 1;
-  } else {
-    const int i = w >> 3;
-    bh = (i / p.bph) * 8 + (w & 7);
-    bin = i % p.bph;
-    nitems = p.ipb;
-    qb0 = 0;
+// (b, h), bin and first query block of this workgroup under a plan
+__device__ __forceinline__ void plan_first(const QPlan& p, int& bh, int& bin, int& qb) {
+  const int i = blockIdx.x >> 3;
+  bh = (i / p.bph) * 8 + (blockIdx.x & 7);
+  bin = i % p.bph;
+  qb = p.blk[bin * p.ipb];
+}
+
+// Query block k of this workgroup's bin (false: none); waits for the previous
+// block's loads and LDS reads
+__device__ __forceinline__ bool plan_next(const QPlan& p, int bin, int k, int& qb) {
+  if (k >= p.ipb || p.blk[bin * p.ipb + k] == PLAN_NONE) return false;
+  qb = p.blk[bin * p.ipb + k];
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  return true;
+}
+
+// Persistent launches.  The hardware hands workgroups to the 8 XCDs round-robin
+// and, inside an XCD, to its 4 shader engines round-robin, strictly in index
+// order: a workgroup waits for a free CU in its own shader engine while other
+// engines sit idle (timeline probes at n = 18432, 8 heads: 22 us of such gaps
+// per CU in the 1.25 ms key-stationary launch), and the XCDs run at different
+// speeds (5-8% apart), which no static assignment can follow.  With more
+// blocks than CUs the grid is therefore one workgroup per CU, and blocks come
+// from 8 queues, one per XCD (workgroup w runs on XCD w % 8): queue x holds the
+// blocks of the (b, h) with bh % 8 == x, heaviest rank first, the (b, h)
+// interleaved within a rank, so an XCD's L2 serves one group of (b, h) at a
+// time.  A workgroup's first block is fixed by its index; after each block
+// thread 0 takes the next entry of its own queue with one device-scope atomic
+// add (about 1.2 us), and once that queue is drained, entries of the other
+// queues, skipping those that a bit mask marks drained.  The last workgroup to
+// find every queue drained returns the counters to zero, so each launch finds
+// them cleared.  Which workgroup runs a block does not change its result:
+// every block is computed whole by one workgroup.
+struct WorkQ {
+  // counters of this launch (nullptr = plain grid): [0, 8) queue heads,
+  // [8] workgroups done, [9] mask of drained queues
+  unsigned* ctr;
+  int slots;  // workgroups per queue (grid / 8); their first blocks are not counted
+};
+
+__device__ __forceinline__ int wq_len(int x, int nblk, int BH) { return BH > x ? ((BH - x + 7) >> 3) * nblk : 0; }
+
+// (b, h) and block of entry j of queue x
+__device__ __forceinline__ void wq_decode(int x, int j, int nblk, int BH, bool heavy_last, int& bh, int& blk) {
+  const int m = (BH - x + 7) >> 3;
+  const int r = j / m;
+  bh = x + 8 * (j - r * m);
+  blk = heavy_last ? nblk - 1 - r : r;
+}
+
+// First block of this workgroup; false when it has none.
+__device__ __forceinline__ bool wq_first(const WorkQ& q, int nblk, int BH, bool heavy_last, int& bh, int& blk) {
+  if (!q.ctr) {
+    schedule(blockIdx.x, nblk, BH, bh, blk, heavy_last);
+    return true;
   }
+  const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
+  if (j >= wq_len(x, nblk, BH)) return false;
+  wq_decode(x, j, nblk, BH, heavy_last, bh, blk);
+  return true;
+}
+
+// Next block of this workgroup (persistent launches; false: none left).  Every
+// thread calls it once the previous block's LDS reads are done; s is two ints
+// of LDS.  The previous block's direct-to-LDS loads are waited for here.
+__device__ __forceinline__ bool wq_next(const WorkQ& q, int nblk, int BH, bool heavy_last, int& bh, int& blk,
+                                        int* s) {
+  if (threadIdx.x == 0) {
+    const int x0 = blockIdx.x & 7;
+    int found = -1, fx = x0;
+    unsigned drained = 0;
+    for (int d = 0; d < 8 && found < 0; ++d) {
+      const int x = (x0 + d) & 7;
+      const int len = wq_len(x, nblk, BH);
+      if (len <= q.slots || ((drained >> x) & 1)) {
+        if (d == 0) drained = atomicOr(q.ctr + 9, 0u);  // no counted entries here: learn which queues are drained
+        continue;
+      }
+      const int j = q.slots + (int)atomicAdd(q.ctr + x, 1u);
+      if (j < len) {
+        found = j;
+        fx = x;
+      } else if (d == 0) {  // own queue drained: mark it, and learn which others are
+        drained = atomicOr(q.ctr + 9, 1u << x);
+      } else {
+        atomicOr(q.ctr + 9, 1u << x);
+      }
+    }
+    if (found < 0 && atomicAdd(q.ctr + 8, 1u) == gridDim.x - 1) {
+#pragma unroll
+      for (int i = 0; i < 10; ++i) atomicExch(q.ctr + i, 0u);
+    }
+    s[0] = found;
+    s[1] = fx;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // all of this wave's loads have landed
+  __syncthreads();
+  const int j = __builtin_amdgcn_readfirstlane(s[0]), x = __builtin_amdgcn_readfirstlane(s[1]);
+  if (j < 0) return false;
+  wq_decode(x, j, nblk, BH, heavy_last, bh, blk);
+  return true;
 }
 
 // ---------------------------------------------------------------------------
@@ -536,23 +627,28 @@ __device__ __forceinline__ void fwd_block(const AttnArgs& a, int bh, int qb, bf1
 }
 
 template <int EPI>
-__global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArgs a, const QPlan p) {
+__global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArgs a, const QPlan p, const WorkQ q) {
   __shared__ __attribute__((aligned(1024))) bf16_t K0[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t K1[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t V0[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t V1[TILE];
-  int bh, bin, nitems, qb;
-  plan_slot(p, blockIdx.x, a.nq, a.BH, bh, bin, nitems, qb);
-  for (int k = 0; k < nitems; ++k) {
-    if (p.bph) {
-      qb = p.blk[bin * p.ipb + k];
-      if (qb == PLAN_NONE) break;
-    }
-    if (k) {  // the previous block's loads have landed and its last tile reads are done
-      wait_loads();
-      __syncthreads();
-    }
+  __shared__ int wq_s[2];
+  int bh, qb, bin = 0;
+  bool have;
+  if (p.bph) {
+    plan_first(p, bh, bin, qb);
+    have = qb != PLAN_NONE;
+  } else {
+    have = wq_first(q, a.nq, a.BH, true, bh, qb);
+    if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, true, bh, qb, wq_s);
+  }
+  for (int k = 1; have; ++k) {
     fwd_block<EPI>(a, bh, qb, K0, K1, V0, V1);
+    // the next block starts after this one's last tile reads
+    if (p.bph)
+      have = plan_next(p, bin, k, qb);
+    else
+      have = q.ctr && wq_next(q, a.nq, a.BH, true, bh, qb, wq_s);
   }
 }
 
@@ -680,23 +776,28 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, int bh, int qb, bf16
   store_rows_bf16(a.dq + ((int64_t)bh * n + my_q) * LH_D, acc, a.scale, hh);
 }
 
-__global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const AttnArgs a, const QPlan p) {
+__global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const AttnArgs a, const QPlan p, const WorkQ q) {
   __shared__ __attribute__((aligned(1024))) bf16_t K0[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t K1[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t V0[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t V1[TILE];
-  int bh, bin, nitems, qb;
-  plan_slot(p, blockIdx.x, a.nq, a.BH, bh, bin, nitems, qb);
-  for (int k = 0; k < nitems; ++k) {
-    if (p.bph) {
-      qb = p.blk[bin * p.ipb + k];
-      if (qb == PLAN_NONE) break;
-    }
-    if (k) {  // the previous block's loads have landed and its last tile reads are done
-      wait_loads();
-      __syncthreads();
-    }
+  __shared__ int wq_s[2];
+  int bh, qb, bin = 0;
+  bool have;
+  if (p.bph) {
+    plan_first(p, bh, bin, qb);
+    have = qb != PLAN_NONE;
+  } else {
+    have = wq_first(q, a.nq, a.BH, true, bh, qb);
+    if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, true, bh, qb, wq_s);
+  }
+  for (int k = 1; have; ++k) {
     dq_block(a, bh, qb, K0, K1, V0, V1);
+    // the next block starts after this one's last tile reads
+    if (p.bph)
+      have = plan_next(p, bin, k, qb);
+    else
+      have = q.ctr && wq_next(q, a.nq, a.BH, true, bh, qb, wq_s);
   }
 }
 
@@ -891,196 +992,206 @@ __device__ __forceinline__ void dw_mma(floatx16 (&dp)[2], floatx16 (&dka)[4], co
 }
 
 template <bool GATHER>
-__global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a, const WorkQ q) {
   __shared__ __attribute__((aligned(1024))) bf16_t Q0[TILE], Q1[TILE], Q2[TILE], Q3[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t D0[TILE], D1[TILE], D2[TILE], D3[TILE];
   __shared__ __attribute__((aligned(16))) float L0[2 * BN], L1[2 * BN], L2[2 * BN], L3[2 * BN];  // lse, delta
   __shared__ u32x4 EX[4][4][64];  // P handed from each P wave to its dS wave
   __shared__ __attribute__((aligned(16))) int IX[4][BN];  // selected-row indices of the Q tiles to copy
+  __shared__ int wq_s[2];
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = wave >> 2, pair = wave & 3;
   const LaneLds ll = lane_lds(lane);
   int bh, kblk;
-  schedule(blockIdx.x, a.nq, a.BH, bh, kblk, false);  // early key blocks see the most queries
-  // wave-uniform by construction; said explicitly, or the compiler keeps bh * n (and the
-  // addresses derived from it) in vector registers and spills them across the loop
-  bh = __builtin_amdgcn_readfirstlane(bh);
-  kblk = __builtin_amdgcn_readfirstlane(kblk);
-  const int n = a.n;
-  const BhRows m = bh_rows(a, bh);
-  const int k0 = kblk * BMK, kw = k0 + 32 * pair, my_k = kw + l32;
+  bool have = wq_first(q, a.nq, a.BH, false, bh, kblk);  // early key blocks see the most queries
+  if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, false, bh, kblk, wq_s);
+  while (have) {
+    // wave-uniform by construction; said explicitly, or the compiler keeps bh * n (and the
+    // addresses derived from it) in vector registers and spills them across the loop
+    bh = __builtin_amdgcn_readfirstlane(bh);
+    kblk = __builtin_amdgcn_readfirstlane(kblk);
+    const int n = a.n;
+    const BhRows m = bh_rows(a, bh);
+    const int k0 = kblk * BMK, kw = k0 + 32 * pair, my_k = kw + l32;
 
-  u32x4 kf[8];  // K (P wave) or -V (dS wave) rows of this lane's key
-  {
-    bool pooled;
-    const uint32_t o = row_off(m, my_k, pooled) + 8 * hh;
-    const bf16_t* p = grp ? (pooled ? m.vp : m.v) + o : (pooled ? m.kp : m.k) + o;
+    u32x4 kf[8];  // K (P wave) or -V (dS wave) rows of this lane's key
+    {
+      bool pooled;
+      const uint32_t o = row_off(m, my_k, pooled) + 8 * hh;
+      const bf16_t* p = grp ? (pooled ? m.vp : m.v) + o : (pooled ? m.kp : m.k) + o;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) kf[c] = ldg16(p + 16 * c);
-    if (grp) {  // the dS waves hold -V (bf16 sign flips are exact)
+      for (int c = 0; c < 8; ++c) kf[c] = ldg16(p + 16 * c);
+      if (grp) {  // the dS waves hold -V (bf16 sign flips are exact)
 #pragma unroll
-      for (int c = 0; c < 8; ++c) kf[c] ^= 0x80008000u;
-    }
-  }
-  const int64_t bhn = (int64_t)bh * n;
-  const bf16_t* dbase = a.dout + bhn * LH_D;
-  const float* lse_row = a.lse_in + bhn;
-  const float* dlt_row = a.delta + bhn;
-  const int jt0 = k0 / BN;  // first query tile that sees these keys
-  const int nt = (n + BN - 1) / BN;
-
-  // Copies.  The P waves copy the Q tiles (+ lse on wave 0, the Q row indices
-  // of a later tile on wave 1), the dS waves the dO tiles (+ delta on wave 4),
-  // each wave 16 rows, in their VALU phases: in step j the P waves copy tile
-  // j + 2 (phase 2j + 1) and the dS waves tile j + 3 (phase 2j + 2), each into
-  // the buffer last read in phase 2j - 1 (Q, lse) or 2j (dO, delta); every
-  // wave waits for its previous step's copies before the barrier closing its
-  // VALU phase, so tile t is in LDS from phase 2t on (Q) or 2t + 1 on (dO).
-  // Here: Q tiles jt0, jt0 + 1, dO tiles jt0 .. jt0 + 2, and the indices of
-  // Q tiles jt0 + 2, jt0 + 3.
-  if (grp == 0) {
-    int r[4];
-    rows16<GATHER>(r, m, jt0 * BN, pair, lane);
-    copy_q16(Q0, m, r, pair, lane);
-    rows16<GATHER>(r, m, (jt0 + 1) * BN, pair, lane);
-    copy_q16(Q1, m, r, pair, lane);
-    if (pair == 0) {
-      g2l4(lse_row + min(jt0 * BN + lane, n - 1), L0);
-      g2l4(lse_row + min((jt0 + 1) * BN + lane, n - 1), L1);
-    }
-    if (GATHER && pair == 1) {
-      g2l4(m.idx + min((jt0 + 2) * BN + lane, m.last), IX[2]);
-      g2l4(m.idx + min((jt0 + 3) * BN + lane, m.last), IX[3]);
-    }
-  } else {
-    copy_d16(D0, dbase, jt0 * BN, n, pair, lane);
-    copy_d16(D1, dbase, (jt0 + 1) * BN, n, pair, lane);
-    copy_d16(D2, dbase, (jt0 + 2) * BN, n, pair, lane);
-    if (pair == 0) {
-      g2l4(dlt_row + min(jt0 * BN + lane, n - 1), L0 + BN);
-      g2l4(dlt_row + min((jt0 + 1) * BN + lane, n - 1), L1 + BN);
-      g2l4(dlt_row + min((jt0 + 2) * BN + lane, n - 1), L2 + BN);
-    }
-  }
-  // the first step's dV / dK terms multiply zeros with buffer 3: make it finite
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    reinterpret_cast<u32x4*>(Q3)[tid + 512 * i] = u32x4{};
-    reinterpret_cast<u32x4*>(D3)[tid + 512 * i] = u32x4{};
-  }
-  wait_loads();  // the first tiles and the zeros are in LDS
-  block_barrier();
-
-  floatx16 acc[4];  // dV (P wave) or dK (dS wave)
-#pragma unroll
-  for (int d = 0; d < 4; ++d) acc[d] = floatx16{};
-  floatx16 sc[2] = {floatx16{}, floatx16{}};  // S - lse/(scale log2 e) (P wave) or delta - dP (dS wave)
-  u32x4 op[2][2] = {{u32x4{}, u32x4{}}, {u32x4{}, u32x4{}}};  // P or dS, bf16 operands
-  const float sl2 = a.sl2, nisl2 = -1.0f / a.sl2;
-
-  // Step j: MFMA phase (tile j, and the previous tile's accumulation), then the
-  // VALU phase with this step's copies.  The step count is rounded up to a
-  // multiple of 4 so that the buffers rotate statically; steps past the last
-  // tile copy clamped rows.  Each role runs its own loop (same barrier count)
-  // and is register-allocated on its own.
-  auto pstep = [&](int j, const bf16_t* Qc, const float* Lc, const bf16_t* Dp, bf16_t* Qn, float* Ln,
-                   const int* ixc, int* ixn) {
-    __builtin_amdgcn_s_setprio(1);
-    pw_mma(sc, acc, kf, op, Qc, Dp, ll, Lc, nisl2);
-    __builtin_amdgcn_s_setprio(0);
-    block_barrier();
-    {  // copy Q tile j + 2 (indices staged two steps ago), its lse, and the indices of tile j + 4
-      int r[4];
-      if (GATHER)
-        rows16_lds(r, ixc, pair, lane);
-      else
-        rows16<false>(r, m, (j + 2) * BN, pair, lane);
-      copy_q16(Qn, m, r, pair, lane);
-      if (pair == 0) g2l4(lse_row + min((j + 2) * BN + lane, n - 1), Ln);
-      if (GATHER && pair == 1) g2l4(m.idx + min((j + 4) * BN + lane, m.last), ixn);
-    }
-    if (j < nt) {  // P = exp2(S sl2 - lse), masked causally and past n
-      const int q0t = j * BN;
-      const bool mask = q0t < kw + 31 || q0t + BN > n;
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        if (mask) {
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int q = q0t + qb * 32 + slot_key(v, hh);
-            if (my_k > q || q >= n) sc[qb][v] = -INFINITY;
-          }
-        }
-#pragma unroll
-        for (int v = 0; v < 16; ++v) sc[qb][v] = ex2(sc[qb][v] * sl2);
-        op[qb][0] = pack_frag(sc[qb], 0);
-        op[qb][1] = pack_frag(sc[qb], 1);
+        for (int c = 0; c < 8; ++c) kf[c] ^= 0x80008000u;
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) EX[pair][i][lane] = op[i >> 1][i & 1];
-    } else {  // past the last tile the accumulation steps add zeros
-      op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
     }
-    // all but this step's copies have landed
-    if (pair == 0 || (GATHER && pair == 1))
-      wait_vm<5>();
-    else
-      wait_vm<4>();
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this phase's LDS writes have landed
-    block_barrier();
-  };
-  auto dstep = [&](int j, const bf16_t* Dc, const float* Lc, const bf16_t* Qp, bf16_t* Dn, float* Ln) {
-    __builtin_amdgcn_s_setprio(1);
-    dw_mma(sc, acc, kf, op, Dc, Qp, ll, Lc + BN);
-    __builtin_amdgcn_s_setprio(0);
-    block_barrier();
-    copy_d16(Dn, dbase, (j + 3) * BN, n, pair, lane);  // dO tile j + 3 and its delta
-    if (pair == 0) g2l4(dlt_row + min((j + 3) * BN + lane, n - 1), Ln + BN);
-    if (j < nt) {  // dS = P (dP - delta), P from the partner P wave
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        const u32x4 e0 = EX[pair][2 * qb][lane], e1 = EX[pair][2 * qb + 1][lane];
-        float pv[16];
-        unpack8(uint4{e0.x, e0.y, e0.z, e0.w}, pv);
-        unpack8(uint4{e1.x, e1.y, e1.z, e1.w}, pv + 8);
-#pragma unroll
-        for (int v = 0; v < 16; ++v) sc[qb][v] = pv[v] * -sc[qb][v];  // P (dP - delta)
-        op[qb][0] = pack_frag(sc[qb], 0);
-        op[qb][1] = pack_frag(sc[qb], 1);
+    const int64_t bhn = (int64_t)bh * n;
+    const bf16_t* dbase = a.dout + bhn * LH_D;
+    const float* lse_row = a.lse_in + bhn;
+    const float* dlt_row = a.delta + bhn;
+    const int jt0 = k0 / BN;  // first query tile that sees these keys
+    const int nt = (n + BN - 1) / BN;
+
+    // Copies.  The P waves copy the Q tiles (+ lse on wave 0, the Q row indices
+    // of a later tile on wave 1), the dS waves the dO tiles (+ delta on wave 4),
+    // each wave 16 rows, in their VALU phases: in step j the P waves copy tile
+    // j + 2 (phase 2j + 1) and the dS waves tile j + 3 (phase 2j + 2), each into
+    // the buffer last read in phase 2j - 1 (Q, lse) or 2j (dO, delta); every
+    // wave waits for its previous step's copies before the barrier closing its
+    // VALU phase, so tile t is in LDS from phase 2t on (Q) or 2t + 1 on (dO).
+    // Here: Q tiles jt0, jt0 + 1, dO tiles jt0 .. jt0 + 2, and the indices of
+    // Q tiles jt0 + 2, jt0 + 3.
+    if (grp == 0) {
+      int r[4];
+      rows16<GATHER>(r, m, jt0 * BN, pair, lane);
+      copy_q16(Q0, m, r, pair, lane);
+      rows16<GATHER>(r, m, (jt0 + 1) * BN, pair, lane);
+      copy_q16(Q1, m, r, pair, lane);
+      if (pair == 0) {
+        g2l4(lse_row + min(jt0 * BN + lane, n - 1), L0);
+        g2l4(lse_row + min((jt0 + 1) * BN + lane, n - 1), L1);
+      }
+      if (GATHER && pair == 1) {
+        g2l4(m.idx + min((jt0 + 2) * BN + lane, m.last), IX[2]);
+        g2l4(m.idx + min((jt0 + 3) * BN + lane, m.last), IX[3]);
       }
     } else {
-      op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
+      copy_d16(D0, dbase, jt0 * BN, n, pair, lane);
+      copy_d16(D1, dbase, (jt0 + 1) * BN, n, pair, lane);
+      copy_d16(D2, dbase, (jt0 + 2) * BN, n, pair, lane);
+      if (pair == 0) {
+        g2l4(dlt_row + min(jt0 * BN + lane, n - 1), L0 + BN);
+        g2l4(dlt_row + min((jt0 + 1) * BN + lane, n - 1), L1 + BN);
+        g2l4(dlt_row + min((jt0 + 2) * BN + lane, n - 1), L2 + BN);
+      }
     }
-    if (pair == 0)
-      wait_vm<5>();
-    else
-      wait_vm<4>();
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the partner's P was read
+    // the first step's dV / dK terms multiply zeros with buffer 3: make it finite
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      reinterpret_cast<u32x4*>(Q3)[tid + 512 * i] = u32x4{};
+      reinterpret_cast<u32x4*>(D3)[tid + 512 * i] = u32x4{};
+    }
+    wait_loads();  // the first tiles and the zeros are in LDS
     block_barrier();
-  };
-  if (grp == 0) {
-    for (int j = jt0; j <= nt; j += 4) {
-      pstep(j, Q0, L0, D3, Q2, L2, IX[2], IX[0]);
-      pstep(j + 1, Q1, L1, D0, Q3, L3, IX[3], IX[1]);
-      pstep(j + 2, Q2, L2, D1, Q0, L0, IX[0], IX[2]);
-      pstep(j + 3, Q3, L3, D2, Q1, L1, IX[1], IX[3]);
+
+    floatx16 acc[4];  // dV (P wave) or dK (dS wave)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) acc[d] = floatx16{};
+    floatx16 sc[2] = {floatx16{}, floatx16{}};  // S - lse/(scale log2 e) (P wave) or delta - dP (dS wave)
+    u32x4 op[2][2] = {{u32x4{}, u32x4{}}, {u32x4{}, u32x4{}}};  // P or dS, bf16 operands
+    const float sl2 = a.sl2, nisl2 = -1.0f / a.sl2;
+
+    // Step j: MFMA phase (tile j, and the previous tile's accumulation), then the
+    // VALU phase with this step's copies.  The step count is rounded up to a
+    // multiple of 4 so that the buffers rotate statically; steps past the last
+    // tile copy clamped rows.  Each role runs its own loop (same barrier count)
+    // and is register-allocated on its own.
+    auto pstep = [&](int j, const bf16_t* Qc, const float* Lc, const bf16_t* Dp, bf16_t* Qn, float* Ln,
+                     const int* ixc, int* ixn) {
+      __builtin_amdgcn_s_setprio(1);
+      pw_mma(sc, acc, kf, op, Qc, Dp, ll, Lc, nisl2);
+      __builtin_amdgcn_s_setprio(0);
+      block_barrier();
+      {  // copy Q tile j + 2 (indices staged two steps ago), its lse, and the indices of tile j + 4
+        int r[4];
+        if (GATHER)
+          rows16_lds(r, ixc, pair, lane);
+        else
+          rows16<false>(r, m, (j + 2) * BN, pair, lane);
+        copy_q16(Qn, m, r, pair, lane);
+        if (pair == 0) g2l4(lse_row + min((j + 2) * BN + lane, n - 1), Ln);
+        if (GATHER && pair == 1) g2l4(m.idx + min((j + 4) * BN + lane, m.last), ixn);
+      }
+      if (j < nt) {  // P = exp2(S sl2 - lse), masked causally and past n
+        const int q0t = j * BN;
+        const bool mask = q0t < kw + 31 || q0t + BN > n;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          if (mask) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const int q = q0t + qb * 32 + slot_key(v, hh);
+              if (my_k > q || q >= n) sc[qb][v] = -INFINITY;
+            }
+          }
+#pragma unroll
+          for (int v = 0; v < 16; ++v) sc[qb][v] = ex2(sc[qb][v] * sl2);
+          op[qb][0] = pack_frag(sc[qb], 0);
+          op[qb][1] = pack_frag(sc[qb], 1);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) EX[pair][i][lane] = op[i >> 1][i & 1];
+      } else {  // past the last tile the accumulation steps add zeros
+        op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
+      }
+      // all but this step's copies have landed
+      if (pair == 0 || (GATHER && pair == 1))
+        wait_vm<5>();
+      else
+        wait_vm<4>();
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this phase's LDS writes have landed
+      block_barrier();
+    };
+    auto dstep = [&](int j, const bf16_t* Dc, const float* Lc, const bf16_t* Qp, bf16_t* Dn, float* Ln) {
+      __builtin_amdgcn_s_setprio(1);
+      dw_mma(sc, acc, kf, op, Dc, Qp, ll, Lc + BN);
+      __builtin_amdgcn_s_setprio(0);
+      block_barrier();
+      copy_d16(Dn, dbase, (j + 3) * BN, n, pair, lane);  // dO tile j + 3 and its delta
+      if (pair == 0) g2l4(dlt_row + min((j + 3) * BN + lane, n - 1), Ln + BN);
+      if (j < nt) {  // dS = P (dP - delta), P from the partner P wave
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          const u32x4 e0 = EX[pair][2 * qb][lane], e1 = EX[pair][2 * qb + 1][lane];
+          float pv[16];
+          unpack8(uint4{e0.x, e0.y, e0.z, e0.w}, pv);
+          unpack8(uint4{e1.x, e1.y, e1.z, e1.w}, pv + 8);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) sc[qb][v] = pv[v] * -sc[qb][v];  // P (dP - delta)
+          op[qb][0] = pack_frag(sc[qb], 0);
+          op[qb][1] = pack_frag(sc[qb], 1);
+        }
+      } else {
+        op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
+      }
+      if (pair == 0)
+        wait_vm<5>();
+      else
+        wait_vm<4>();
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the partner's P was read
+      block_barrier();
+    };
+    if (grp == 0) {
+      for (int j = jt0; j <= nt; j += 4) {
+        pstep(j, Q0, L0, D3, Q2, L2, IX[2], IX[0]);
+        pstep(j + 1, Q1, L1, D0, Q3, L3, IX[3], IX[1]);
+        pstep(j + 2, Q2, L2, D1, Q0, L0, IX[0], IX[2]);
+        pstep(j + 3, Q3, L3, D2, Q1, L1, IX[1], IX[3]);
+      }
+      block_barrier();
+    } else {
+      block_barrier();  // the dS waves run one phase behind
+      for (int j = jt0; j <= nt; j += 4) {
+        dstep(j, D0, L0, Q3, D3, L3);
+        dstep(j + 1, D1, L1, Q0, D0, L0);
+        dstep(j + 2, D2, L2, Q1, D1, L1);
+        dstep(j + 3, D3, L3, Q2, D2, L2);
+      }
     }
-    block_barrier();
-  } else {
-    block_barrier();  // the dS waves run one phase behind
-    for (int j = jt0; j <= nt; j += 4) {
-      dstep(j, D0, L0, Q3, D3, L3);
-      dstep(j + 1, D1, L1, Q0, D0, L0);
-      dstep(j + 2, D2, L2, Q1, D1, L1);
-      dstep(j + 3, D3, L3, Q2, D2, L2);
+    if (my_k < n) {
+      // the row addresses are formed here, not held through the loops (they would spill)
+      int row = my_k, half = hh;
+      asm volatile("" : "+v"(row), "+v"(half));
+      if (grp == 0)
+        store_rows_bf16(a.dv + ((int64_t)bh * n + row) * LH_D, acc, 1.0f, half);
+      else
+        store_rows_bf16(a.dk + ((int64_t)bh * n + row) * LH_D, acc, a.scale, half);
     }
+    if (!q.ctr) break;
+    have = wq_next(q, a.nq, a.BH, false, bh, kblk, wq_s);  // the previous block's copies are waited for there
   }
-  if (my_k >= n) return;
-  if (grp == 0)
-    store_rows_bf16(a.dv + ((int64_t)bh * n + my_k) * LH_D, acc, 1.0f, hh);
-  else
-    store_rows_bf16(a.dk + ((int64_t)bh * n + my_k) * LH_D, acc, a.scale, hh);
 }
 
 // ===========================================================================
@@ -1555,6 +1666,62 @@ int make_plan(int BH, int n, QPlan& p) {
   return p.bph ? p.bph * BH : plain;
 }
 
+// Work-queue counters of the persistent launches: one 128-byte slot per
+// (device, stream), so launches that may run at the same time (different
+// streams) never share counters, while launches on one stream run one after
+// the other and each leaves its slot cleared.  A launch captured into a graph
+// keeps the slot of the stream it was captured on.  Past WQ_SLOTS streams on a
+// device, launches fall back to the plain grid.
+constexpr int WQ_SLOTS = 64, WQ_STRIDE = 32;
+__device__ __attribute__((aligned(256))) unsigned g_wq[WQ_SLOTS * WQ_STRIDE];
+
+unsigned* wq_counters(hipStream_t st) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  static std::mutex mu;
+  static unsigned* base[64];
+  static int used[64];
+  static std::map<std::pair<int, std::pair<uintptr_t, std::thread::id>>, int> slot;
+  std::lock_guard<std::mutex> g(mu);
+  if (!base[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_wq)) != hipSuccess || !ptr) return nullptr;
+    base[dev] = static_cast<unsigned*>(ptr);
+  }
+  // hipStreamPerThread names a different stream on every host thread
+  const std::thread::id tid = st == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
+  const auto key = std::make_pair(dev, std::make_pair(reinterpret_cast<uintptr_t>(st), tid));
+  auto it = slot.find(key);
+  if (it != slot.end()) return base[dev] + it->second * WQ_STRIDE;
+  if (used[dev] == WQ_SLOTS) return nullptr;
+  slot[key] = used[dev];
+  return base[dev] + (used[dev]++) * WQ_STRIDE;
+}
+
+// Grid of a launch over BH (b, h) of nblk blocks each: one workgroup per CU
+// with work queues when there are more blocks than CUs, else one block per
+// workgroup.
+int wq_grid(int nblk, int BH, hipStream_t st, WorkQ& q) {
+  q.ctr = nullptr;
+  q.slots = 0;
+  const long long total = (long long)nblk * BH;
+  const int cus = cu_count();
+  if (cus <= 0 || cus % 8 || total <= cus) return (int)total;
+  unsigned* c = wq_counters(st);
+  if (!c) return (int)total;
+  q.ctr = c;
+  q.slots = cus / 8;
+  return cus;
+}
+
+// Grid of a query-stationary launch: a packed plan where one applies, else as wq_grid.
+int query_grid(int BH, int n, hipStream_t st, QPlan& p, WorkQ& q) {
+  const int grid = make_plan(BH, n, p);
+  q.ctr = nullptr;
+  q.slots = 0;
+  return p.bph ? grid : wq_grid((n + 32 * QW - 1) / (32 * QW), BH, st, q);
+}
+
 }  // namespace
 
 extern "C" int lh_attn_fwd(const void* q, const void* k, const void* v, int64_t sb, int64_t ss, int64_t sh,
@@ -1566,9 +1733,11 @@ extern "C" int lh_attn_fwd(const void* q, const void* k, const void* v, int64_t 
   if (rc) return rc;
   if (!out || !lse || !al16(out)) return LH_ERR_INVALID_ARG;
   a.out = (bf16_t*)out; a.lse = lse;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   QPlan p;
-  const int grid = make_plan(a.BH, a.n, p);
-  hipLaunchKernelGGL(attn_fwd_kernel<0>, dim3(grid), dim3(64 * QW), 0, reinterpret_cast<hipStream_t>(stream), a, p);
+  WorkQ wq;
+  const int grid = query_grid(a.BH, a.n, st, p, wq);
+  hipLaunchKernelGGL(attn_fwd_kernel<0>, dim3(grid), dim3(64 * QW), 0, st, a, p, wq);
   LH_CHECK_LAUNCH();
   return LH_OK;
 }
@@ -1592,16 +1761,19 @@ int attn_bwd_parts(int parts, const void* q, const void* k, const void* v, int64
   if (parts & 1) {
     AttnArgs ak = a;
     ak.nq = (a.n + BMK - 1) / BMK;
+    WorkQ wq;
+    const int grid = wq_grid(ak.nq, ak.BH, st, wq);
     if (indices)
-      hipLaunchKernelGGL(attn_bwd_dkdv_kernel<true>, dim3(ak.nq * ak.BH), dim3(512), 0, st, ak);
+      hipLaunchKernelGGL(attn_bwd_dkdv_kernel<true>, dim3(grid), dim3(512), 0, st, ak, wq);
     else
-      hipLaunchKernelGGL(attn_bwd_dkdv_kernel<false>, dim3(ak.nq * ak.BH), dim3(512), 0, st, ak);
+      hipLaunchKernelGGL(attn_bwd_dkdv_kernel<false>, dim3(grid), dim3(512), 0, st, ak, wq);
     LH_CHECK_LAUNCH();
   }
   if (parts & 2) {
     QPlan p;
-    const int grid = make_plan(a.BH, a.n, p);
-    hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3(grid), dim3(64 * QW), 0, st, a, p);
+    WorkQ wq;
+    const int grid = query_grid(a.BH, a.n, st, p, wq);
+    hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3(grid), dim3(64 * QW), 0, st, a, p, wq);
     LH_CHECK_LAUNCH();
   }
   return LH_OK;
@@ -1653,8 +1825,9 @@ extern "C" int lh_dilated_scores(const void* xq, const void* xk, const void* xv,
     a.scores = pass == 0 ? scores_qk : scores_kq;
     a.Ho = H; a.dil = dilation; a.S_tot = S_tot;
     QPlan p;
-    const int grid = make_plan(a.BH, a.n, p);
-    hipLaunchKernelGGL(attn_fwd_kernel<1>, dim3(grid), dim3(64 * QW), 0, st, a, p);
+    WorkQ wq;
+    const int grid = query_grid(a.BH, a.n, st, p, wq);
+    hipLaunchKernelGGL(attn_fwd_kernel<1>, dim3(grid), dim3(64 * QW), 0, st, a, p, wq);
     LH_CHECK_LAUNCH();
   }
   return LH_OK;

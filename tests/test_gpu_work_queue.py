@@ -1,12 +1,20 @@
-"""Query-block plans of the query-stationary attention kernels.
+"""Work queues and block plans of the attention launches.
 
-With B*H a multiple of 8 and between 1 and 3.5 query blocks per CU of a (b, h),
-the forward and dQ kernels run one workgroup per CU, each taking a host-packed
-list of query blocks (lh_attn.hip, make_plan / plan_slot) instead of one block
-per workgroup.  Per-block arithmetic is unchanged, so results must be bit-equal
-to the same heads run one at a time (B*H = 1: no plan).  The oracle checks of
-these kernels at full size (test_gpu_configs.py) run with plans where these
-conditions hold (cfg2, cfg3 at k = 1536 and 3072, cfg4's selected attention).
+With more blocks than CUs the attention kernels run one workgroup per CU.  The
+query-stationary kernels (forward, dQ) take a host-packed list of query blocks
+when B*H is a multiple of 8 and a (b, h) has 1 to 3.5 blocks per CU (lh_attn.hip,
+make_plan / plan_first / plan_next); otherwise, and always for dK/dV, the
+workgroups take blocks from 8 per-XCD queues through device-scope atomic
+counters that the last workgroup clears (wq_first / wq_next / wq_grid).  Which
+workgroup runs a block does not change its arithmetic, so results must be
+bit-equal to the same heads run one at a time, and every launch must find the
+counters cleared by the one before (each test launches many times on one
+stream; one case runs on two streams).  B*H below 8 leaves queues empty, so
+those XCDs' workgroups start by taking blocks from the other queues.  Cases:
+(9001, 1, 8), (12345, 2, 4), (8448, 1, 16) and the dilated scorer use plans for
+the forward and dQ; (30000, 1, 3) and dense (30000, 1, 8) use queues for all
+three kernels.  The oracle checks at full size (test_gpu_configs.py) run
+with whichever applies.
 """
 import pytest
 import torch
@@ -20,7 +28,7 @@ def _rand(shape, seed, dev):
 
 
 def _per_head(pkg, xs, pxs, idx, split, B, H, n, do, lse_all, delta_all):
-    """O, lse, dq, dk, dv of every (b, h) computed alone (B = H = 1: no plan)."""
+    """O, lse, dq, dk, dv of every (b, h) computed alone (B = H = 1)."""
     N = pkg._native
     outs = {k: [] for k in ("o", "lse", "dq", "dk", "dv")}
     for b in range(B):
@@ -43,10 +51,10 @@ def _per_head(pkg, xs, pxs, idx, split, B, H, n, do, lse_all, delta_all):
     return {k: torch.cat(v, 1).reshape(B, H, *v[0].shape[2:]) for k, v in outs.items()}
 
 
-@pytest.mark.parametrize("n,B,H", [(9001, 1, 8), (12345, 2, 4), (8448, 1, 16)])
-def test_plan_gathered_bit_equal(pkg, dev, n, B, H):
+@pytest.mark.parametrize("n,B,H", [(9001, 1, 8), (12345, 2, 4), (8448, 1, 16), (30000, 1, 3)])
+def test_queue_gathered_bit_equal(pkg, dev, n, B, H):
     """Gathered rows (random distinct base and pooled rows), ragged n (partial last block)."""
-    print(f"plan gathered n={n} B={B} H={H}", flush=True)
+    print(f"queues gathered n={n} B={B} H={H}", flush=True)
     N = pkg._native
     S, Sp = n, n // 3
     xs = [_rand((B, S, H, 128), 10 + i, dev) for i in range(3)]
@@ -62,13 +70,13 @@ def test_plan_gathered_bit_equal(pkg, dev, n, B, H):
     dq, dk, dv = N.attn_bwd(rows, idx, B, H, n, do, lse, delta)
     ref = _per_head(pkg, xs, pxs, idx, S, B, H, n, do, lse, delta)
     for name, got in (("o", o), ("lse", lse), ("dq", dq), ("dk", dk), ("dv", dv)):
-        assert torch.equal(got, ref[name]), f"{name} differs from the per-head (no plan) result"
+        assert torch.equal(got, ref[name]), f"{name} differs from the per-head result"
 
 
-@pytest.mark.parametrize("n,B,H", [(10000, 2, 4)])
-def test_plan_dense_bit_equal(pkg, dev, n, B, H):
+@pytest.mark.parametrize("n,B,H", [(10000, 2, 4), (30000, 1, 8)])
+def test_queue_dense_bit_equal(pkg, dev, n, B, H):
     """Identity row map (the dense layers' path)."""
-    print(f"plan dense n={n} B={B} H={H}", flush=True)
+    print(f"queues dense n={n} B={B} H={H}", flush=True)
     N = pkg._native
     xs = [_rand((B, n, H, 128), 40 + i, dev) for i in range(3)]
     rows = N.Rows(*xs, (xs[0].stride(0), xs[0].stride(1), xs[0].stride(2)))
@@ -78,13 +86,13 @@ def test_plan_dense_bit_equal(pkg, dev, n, B, H):
     dq, dk, dv = N.attn_bwd(rows, None, B, H, n, do, lse, delta)
     ref = _per_head(pkg, xs, None, None, None, B, H, n, do, lse, delta)
     for name, got in (("o", o), ("lse", lse), ("dq", dq), ("dk", dk), ("dv", dv)):
-        assert torch.equal(got, ref[name]), f"{name} differs from the per-head (no plan) result"
+        assert torch.equal(got, ref[name]), f"{name} differs from the per-head result"
 
 
-def test_plan_dilated_scores_bit_equal(pkg, dev):
-    """Dilated scorer: 8 heads x dilation 4 = 32 virtual heads of 4096 tokens (8 bins of 2 blocks per head)."""
+def test_queue_dilated_scores_bit_equal(pkg, dev):
+    """Dilated scorer: 8 heads x dilation 4 = 32 virtual heads of 16 query blocks (512 blocks)."""
     S, H, dil, L, p = 16384, 8, 4, 3, 4
-    print(f"plan dilated S={S} H={H} dil={dil}", flush=True)
+    print(f"queues dilated S={S} H={H} dil={dil}", flush=True)
     N = pkg._native
     xs = [_rand((1, S, H, 128), 60 + i, dev) for i in range(3)]
     _, _, S_tot = N.pyramid_lengths(S, L, p)
@@ -94,3 +102,29 @@ def test_plan_dilated_scores_bit_equal(pkg, dev):
         rq, rk = N.dilated_scores(*sl, dil, S_tot)
         assert torch.equal(sqk[:, h:h + 1, :S], rq[..., :S]), f"head {h}: qk scores differ"
         assert torch.equal(skq[:, h:h + 1, :S], rk[..., :S]), f"head {h}: kq scores differ"
+
+
+def test_queue_two_streams(pkg, dev):
+    """The same launches on the default stream and a second stream (separate counter slots), three times each."""
+    n, B, H = 20000, 1, 8
+    print(f"queues two streams n={n} B={B} H={H}", flush=True)
+    N = pkg._native
+    xs = [_rand((B, n, H, 128), 70 + i, dev) for i in range(3)]
+    rows = N.Rows(*xs, (xs[0].stride(0), xs[0].stride(1), xs[0].stride(2)))
+    o, lse = N.attn_fwd(rows, None, B, H, n)
+    do = _rand((B, H, n, 128), 80, dev)
+    delta = (do.float() * o.float()).sum(-1)
+    ref = (o, lse) + N.attn_bwd(rows, None, B, H, n, do, lse, delta)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    got = []
+    for r in range(3):
+        with torch.cuda.stream(side):
+            a = N.attn_fwd(rows, None, B, H, n) + N.attn_bwd(rows, None, B, H, n, do, lse, delta)
+        b = N.attn_fwd(rows, None, B, H, n) + N.attn_bwd(rows, None, B, H, n, do, lse, delta)
+        got += [a, b]
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    for i, g in enumerate(got):
+        for name, x, y in zip(("o", "lse", "dq", "dk", "dv"), g, ref):
+            assert torch.equal(x, y), f"launch {i}: {name} differs"
