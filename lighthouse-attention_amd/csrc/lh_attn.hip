@@ -192,9 +192,9 @@ __device__ __forceinline__ bool plan_next(const QPlan& p, int bin, int k, int& q
 // speeds (5-8% apart), which no static assignment can follow.  With more
 // blocks than CUs the grid is therefore one workgroup per CU, and blocks come
 // from 8 queues, one per XCD (workgroup w runs on XCD w % 8): queue x holds the
-// blocks of the (b, h) with bh % 8 == x, heaviest rank first, the (b, h)
-// interleaved within a rank, so an XCD's L2 serves one group of (b, h) at a
-// time.  A workgroup's first block is fixed by its index; after each block
+// blocks of the x-th eighth of the (b, h), bh in [x BH / 8, (x + 1) BH / 8), one
+// (b, h) after the other, heaviest block first within each, so the XCD's CUs
+// sweep the rows of one (b, h) together and share them in its L2.  A workgroup's first block is fixed by its index; after each block
 // thread 0 takes the next entry of its own queue with one device-scope atomic
 // add (about 1.2 us), and once that queue is drained, entries of the other
 // queues, skipping those that a bit mask marks drained.  The last workgroup to
@@ -208,13 +208,14 @@ struct WorkQ {
   int slots;  // workgroups per queue (grid / 8); their first blocks are not counted
 };
 
-__device__ __forceinline__ int wq_len(int x, int nblk, int BH) { return BH > x ? ((BH - x + 7) >> 3) * nblk : 0; }
+// first (b, h) of queue x; queue x holds [wq_lo(x), wq_lo(x + 1))
+__device__ __forceinline__ int wq_lo(int x, int BH) { return (int)(((long long)x * BH) >> 3); }
+__device__ __forceinline__ int wq_len(int x, int nblk, int BH) { return (wq_lo(x + 1, BH) - wq_lo(x, BH)) * nblk; }
 
 // (b, h) and block of entry j of queue x
 __device__ __forceinline__ void wq_decode(int x, int j, int nblk, int BH, bool heavy_last, int& bh, int& blk) {
-  const int m = (BH - x + 7) >> 3;
-  const int r = j / m;
-  bh = x + 8 * (j - r * m);
+  const int i = j / nblk, r = j - i * nblk;
+  bh = wq_lo(x, BH) + i;
   blk = heavy_last ? nblk - 1 - r : r;
 }
 
@@ -1699,14 +1700,16 @@ unsigned* wq_counters(hipStream_t st) {
 }
 
 // Grid of a launch over BH (b, h) of nblk blocks each: one workgroup per CU
-// with work queues when there are more blocks than CUs, else one block per
-// workgroup.
+// with work queues when there are 1 to 12 blocks per CU, else one block per
+// workgroup.  Past 12 the plain grid's gaps and tail are a small share, and the
+// kernels are power-limited, so CUs kept busier run at a lower clock: the
+// dilated scorer at cfg4 (16 blocks per CU) measured 1% slower with queues.
 int wq_grid(int nblk, int BH, hipStream_t st, WorkQ& q) {
   q.ctr = nullptr;
   q.slots = 0;
   const long long total = (long long)nblk * BH;
   const int cus = cu_count();
-  if (cus <= 0 || cus % 8 || total <= cus) return (int)total;
+  if (cus <= 0 || cus % 8 || total <= cus || total > 12LL * cus) return (int)total;
   unsigned* c = wq_counters(st);
   if (!c) return (int)total;
   q.ctr = c;
