@@ -196,6 +196,13 @@ int lh_check_indices(const int32_t *indices, int B, int H, int n, int lo, int hi
  *   out  bf16 [B, H, n, D];  lse fp32 [B, H, n] (log2-domain: m*log2(e)+log2(sum),
  *        sum = the row sum of the bf16-rounded probabilities that weight V, so
  *        the weights of each output row sum to 1 up to fp32 accumulation)
+ * With more blocks than CUs this launch and the backward's run one workgroup
+ * per CU, taking blocks from a host-packed plan or from work-queue counters
+ * that live in the library's device memory, one slot per (device, stream),
+ * which each launch leaves cleared.  Launches on different streams therefore
+ * never share counters; a launch captured into a graph keeps the slot of the
+ * stream it was captured on, so replays of it must not overlap other attention
+ * launches on that stream's slot (replay on the capture stream, or one at a time).
  */
 int lh_attn_fwd(const void *q, const void *k, const void *v, int64_t sb, int64_t ss, int64_t sh,
                 const void *qp, const void *kp, const void *vp, int64_t pb, int64_t ps, int64_t ph,
@@ -204,7 +211,8 @@ int lh_attn_fwd(const void *q, const void *k, const void *v, int64_t sb, int64_t
 
 /*
  * Causal attention backward over gathered rows (deterministic: dK/dV per key
- * block, dQ per query block, no atomics).  Replaces the SDPA backward and the
+ * block, dQ per query block, each output element written by one workgroup;
+ * block scheduling as lh_attn_fwd).  Replaces the SDPA backward and the
  * gather backward's row selection (src/lighthouse_selection.py:800-815).
  *   dout   bf16 [B, H, n, D] (from lh_scatter_bwd); lse, delta fp32 [B, H, n]
  *   dq, dk, dv bf16 [B, H, n, D] in selected order
