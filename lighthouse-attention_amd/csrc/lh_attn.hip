@@ -1091,9 +1091,11 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
     // and is register-allocated on its own.
     auto pstep = [&](int j, const bf16_t* Qc, const float* Lc, const bf16_t* Dp, bf16_t* Qn, float* Ln,
                      const int* ixc, int* ixn) {
-      __builtin_amdgcn_s_setprio(1);
-      pw_mma(sc, acc, kf, op, Qc, Dp, ll, Lc, nisl2);
-      __builtin_amdgcn_s_setprio(0);
+      if (j <= nt) {  // steps past nt (the rounding to 4) would multiply masked tiles and add zeros
+        __builtin_amdgcn_s_setprio(1);
+        pw_mma(sc, acc, kf, op, Qc, Dp, ll, Lc, nisl2);
+        __builtin_amdgcn_s_setprio(0);
+      }
       block_barrier();
       {  // copy Q tile j + 2 (indices staged two steps ago), its lse, and the indices of tile j + 4
         int r[4];
@@ -1136,9 +1138,11 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
       block_barrier();
     };
     auto dstep = [&](int j, const bf16_t* Dc, const float* Lc, const bf16_t* Qp, bf16_t* Dn, float* Ln) {
-      __builtin_amdgcn_s_setprio(1);
-      dw_mma(sc, acc, kf, op, Dc, Qp, ll, Lc + BN);
-      __builtin_amdgcn_s_setprio(0);
+      if (j <= nt) {
+        __builtin_amdgcn_s_setprio(1);
+        dw_mma(sc, acc, kf, op, Dc, Qp, ll, Lc + BN);
+        __builtin_amdgcn_s_setprio(0);
+      }
       block_barrier();
       copy_d16(Dn, dbase, (j + 3) * BN, n, pair, lane);  // dO tile j + 3 and its delta
       if (pair == 0) g2l4(dlt_row + min((j + 3) * BN + lane, n - 1), Ln + BN);
