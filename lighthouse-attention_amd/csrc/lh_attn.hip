@@ -231,16 +231,41 @@ __device__ __forceinline__ bool wq_first(const WorkQ& q, int nblk, int BH, bool 
   return true;
 }
 
-// Next block of this workgroup (persistent launches; false: none left).  Every
-// thread calls it once the previous block's LDS reads are done; s is two ints
-// of LDS.  The previous block's direct-to-LDS loads are waited for here.
-__device__ __forceinline__ bool wq_next(const WorkQ& q, int nblk, int BH, bool heavy_last, int& bh, int& blk,
-                                        int* s) {
+// Thread 0, shortly before its workgroup's block ends: reserve the next entry
+// of the workgroup's own queue.  Returns the counter's old value c (the entry
+// is slots + c, valid while below the queue's length), or -1 when the queue has
+// no counted entries; wq_next takes it as `reserved`.  Its first use is there,
+// so the atomic's latency hides behind the rest of the block.  The address is
+// made per-lane because the compiler's rewrite of a uniform-address atomic
+// reads the result at once.
+__device__ __forceinline__ int wq_reserve(const WorkQ& q, int nblk, int BH) {
+  const int x = blockIdx.x & 7;
+  if (wq_len(x, nblk, BH) <= q.slots) return -1;
+  int zero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+  return (int)atomicAdd(q.ctr + x + zero, 1u);
+}
+
+// Next block of this workgroup (persistent launches; false: none left), from
+// thread 0's reservation (wq_reserve's value; -1: none made) or by taking
+// entries itself.  Every thread calls it once the previous block's LDS reads
+// are done; s is two ints of LDS.  The previous block's direct-to-LDS loads are
+// waited for here.
+__device__ __forceinline__ bool wq_next(const WorkQ& q, int nblk, int BH, bool heavy_last, int reserved, int& bh,
+                                        int& blk, int* s) {
   if (threadIdx.x == 0) {
     const int x0 = blockIdx.x & 7;
     int found = -1, fx = x0;
     unsigned drained = 0;
-    for (int d = 0; d < 8 && found < 0; ++d) {
+    int d = 0;
+    if (reserved >= 0) {  // the own queue was asked already
+      if (q.slots + reserved < wq_len(x0, nblk, BH))
+        found = q.slots + reserved;
+      else
+        drained = atomicOr(q.ctr + 9, 1u << x0);
+      d = 1;
+    }
+    for (; d < 8 && found < 0; ++d) {
       const int x = (x0 + d) & 7;
       const int len = wq_len(x, nblk, BH);
       if (len <= q.slots || ((drained >> x) & 1)) {
@@ -641,7 +666,7 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArg
     have = qb != PLAN_NONE;
   } else {
     have = wq_first(q, a.nq, a.BH, true, bh, qb);
-    if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, true, bh, qb, wq_s);
+    if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, true, -1, bh, qb, wq_s);
   }
   for (int k = 1; have; ++k) {
     fwd_block<EPI>(a, bh, qb, K0, K1, V0, V1);
@@ -649,7 +674,7 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArg
     if (p.bph)
       have = plan_next(p, bin, k, qb);
     else
-      have = q.ctr && wq_next(q, a.nq, a.BH, true, bh, qb, wq_s);
+      have = q.ctr && wq_next(q, a.nq, a.BH, true, -1, bh, qb, wq_s);
   }
 }
 
@@ -790,7 +815,7 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const Attn
     have = qb != PLAN_NONE;
   } else {
     have = wq_first(q, a.nq, a.BH, true, bh, qb);
-    if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, true, bh, qb, wq_s);
+    if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, true, -1, bh, qb, wq_s);
   }
   for (int k = 1; have; ++k) {
     dq_block(a, bh, qb, K0, K1, V0, V1);
@@ -798,7 +823,7 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const Attn
     if (p.bph)
       have = plan_next(p, bin, k, qb);
     else
-      have = q.ctr && wq_next(q, a.nq, a.BH, true, bh, qb, wq_s);
+      have = q.ctr && wq_next(q, a.nq, a.BH, true, -1, bh, qb, wq_s);
   }
 }
 
@@ -1006,7 +1031,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
   const LaneLds ll = lane_lds(lane);
   int bh, kblk;
   bool have = wq_first(q, a.nq, a.BH, false, bh, kblk);  // early key blocks see the most queries
-  if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, false, bh, kblk, wq_s);
+  if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, false, -1, bh, kblk, wq_s);
   while (have) {
     // wave-uniform by construction; said explicitly, or the compiler keeps bh * n (and the
     // addresses derived from it) in vector registers and spills them across the loop
@@ -1168,6 +1193,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the partner's P was read
       block_barrier();
     };
+    int next = -1;  // thread 0: the reserved next entry
     if (grp == 0) {
       for (int j = jt0; j <= nt; j += 4) {
         pstep(j, Q0, L0, D3, Q2, L2, IX[2], IX[0]);
@@ -1175,6 +1201,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
         pstep(j + 2, Q2, L2, D1, Q0, L0, IX[0], IX[2]);
         pstep(j + 3, Q3, L3, D2, Q1, L1, IX[1], IX[3]);
       }
+      // the dS waves' last phase is still to run: reserve the next block now
+      if (q.ctr && threadIdx.x == 0) next = wq_reserve(q, a.nq, a.BH);
       block_barrier();
     } else {
       block_barrier();  // the dS waves run one phase behind
@@ -1195,7 +1223,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
         store_rows_bf16(a.dk + ((int64_t)bh * n + row) * LH_D, acc, a.scale, half);
     }
     if (!q.ctr) break;
-    have = wq_next(q, a.nq, a.BH, false, bh, kblk, wq_s);  // the previous block's copies are waited for there
+    have = wq_next(q, a.nq, a.BH, false, next, bh, kblk, wq_s);  // the previous block's copies are waited for there
   }
 }
 
