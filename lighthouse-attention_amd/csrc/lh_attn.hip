@@ -189,18 +189,19 @@ __device__ __forceinline__ bool plan_next(const QPlan& p, int bin, int k, int& q
 // order: a workgroup waits for a free CU in its own shader engine while other
 // engines sit idle (timeline probes at n = 18432, 8 heads: 22 us of such gaps
 // per CU in the 1.25 ms key-stationary launch), and the XCDs run at different
-// speeds (5-8% apart), which no static assignment can follow.  With more
-// blocks than CUs the grid is therefore one workgroup per CU, and blocks come
-// from 8 queues, one per XCD (workgroup w runs on XCD w % 8): queue x holds the
-// blocks of the x-th eighth of the (b, h), bh in [x BH / 8, (x + 1) BH / 8), one
+// speeds (5-8% apart), which no static assignment can follow.  With more blocks
+// than CUs the grid is therefore one workgroup per CU, and blocks come from 8
+// queues, one per XCD (workgroup w runs on XCD w % 8): queue x holds the blocks
+// of the x-th eighth of the (b, h), bh in [x BH / 8, (x + 1) BH / 8), one
 // (b, h) after the other, heaviest block first within each, so the XCD's CUs
-// sweep the rows of one (b, h) together and share them in its L2.  A workgroup's first block is fixed by its index; after each block
-// thread 0 takes the next entry of its own queue with one device-scope atomic
-// add (about 1.2 us), and once that queue is drained, entries of the other
-// queues, skipping those that a bit mask marks drained.  The last workgroup to
-// find every queue drained returns the counters to zero, so each launch finds
-// them cleared.  Which workgroup runs a block does not change its result:
-// every block is computed whole by one workgroup.
+// sweep the rows of one (b, h) together and share them in its L2.  A
+// workgroup's first block is fixed by its index; after each block (the dK/dV
+// kernel: shortly before) thread 0 takes the next entry of its own queue with
+// one device-scope atomic add (about 1.2 us), and once that queue is drained,
+// entries of the other queues, skipping those that a bit mask marks drained.  The last workgroup to find every queue drained
+// returns the counters to zero, so each launch finds them cleared.  Which
+// workgroup runs a block does not change its result: every block is computed
+// whole by one workgroup.
 struct WorkQ {
   // counters of this launch (nullptr = plain grid): [0, 8) queue heads,
   // [8] workgroups done, [9] mask of drained queues
