@@ -37,6 +37,10 @@ extern "C" {
 #define LH_ERR_DOMAIN 2       /* geometry the reference asserts on or overruns (strict mode) */
 #define LH_ERR_LAUNCH 3       /* the HIP runtime refused a launch */
 #define LH_ERR_UNSUPPORTED 4  /* shape beyond this build's limits (e.g. D != 128) */
+#define LH_ERR_RUNTIME 5      /* a HIP runtime call (synchronize, copy, symbol lookup) failed */
+
+/* The ABI this header declares; lh_abi_version() of a matching library returns it. */
+#define LH_ABI_VERSION 6
 
 #define LH_TIE_REFERENCE 0    /* the reference network: strict compare-exchange only */
 #define LH_TIE_LOWER_INDEX 1  /* ties ordered by lower level-local index */
@@ -44,7 +48,8 @@ extern "C" {
 /* Human-readable name of a return code. */
 const char *lh_strerror(int rc);
 
-/* ABI version of this header (bumped on any signature change). */
+/* ABI version of the library (LH_ABI_VERSION of the header it was built
+ * with; bumped on any signature or error-code change). */
 int lh_abi_version(void);
 
 /*
@@ -124,8 +129,11 @@ int lh_dilated_scores(const void *xq, const void *xk, const void *xv,
  * DilatedLighthouseGLAScorer.forward (src/lighthouse_selection.py:713-734).
  *   xq, xk, xv  bf16 [B, S, H, D] contiguous; gk fp32 [B, S, H] contiguous log gates
  *   (token t of head h is position t / dilation of virtual head (t % dilation) * H + h)
- *   segments   <= 0: automatic; else the number of sequence segments walked in
- *              parallel (clamped to the 64-token chunk count).  Segment s starts
+ *   segments   <= 0: automatic, one per 32 chunks of 64 tokens (at least one),
+ *              from the per-sequence length S / dilation alone, so a sequence's
+ *              scores do not depend on the batch or head count around it; else
+ *              the number of sequence segments walked in parallel (clamped to
+ *              the 64-token chunk count).  Segment s starts
  *              from the combined final states of segments 0..s-1, which a first
  *              pass computes; results agree with the one-segment walk to fp32
  *              rounding of the state (the bf16 scores may differ in the last bit).
@@ -200,9 +208,13 @@ int lh_check_indices(const int32_t *indices, int B, int H, int n, int lo, int hi
  * per CU, taking blocks from a host-packed plan or from work-queue counters
  * that live in the library's device memory, one slot per (device, stream),
  * which each launch leaves cleared.  Launches on different streams therefore
- * never share counters; a launch captured into a graph keeps the slot of the
- * stream it was captured on, so replays of it must not overlap other attention
- * launches on that stream's slot (replay on the capture stream, or one at a time).
+ * never share counters.  A launch made while its stream is being captured into
+ * a graph gets a slot of its own, used by no other launch, so captured graphs
+ * may be replayed on any stream, beside eager launches and other graphs; only
+ * a graph replayed beside itself (two replays of it in flight at once) races.
+ * Each persistent launch checks that its blocks added up and otherwise flags
+ * its slot (a slot not cleared at launch: a launch that never finished, or a
+ * replay that overlapped itself); lh_attn_status reports and resets it.
  */
 int lh_attn_fwd(const void *q, const void *k, const void *v, int64_t sb, int64_t ss, int64_t sh,
                 const void *qp, const void *kp, const void *vp, int64_t pb, int64_t ps, int64_t ph,
@@ -240,6 +252,29 @@ int lh_attn_bwd_dq(const void *q, const void *k, const void *v, int64_t sb, int6
                    int split, const int32_t *indices, int B, int H, int n, int D, float scale,
                    const void *dout, const float *lse, const float *delta,
                    void *dq, void *stream);
+
+/*
+ * Work-queue faults of the persistent attention launches (lh_attn_fwd,
+ * lh_attn_bwd*, lh_dilated_scores) on the current device since the last call.
+ * Waits for the device to go idle (hipDeviceSynchronize), then counts the
+ * counter slots that a launch flagged (its blocks did not add up: entries were
+ * skipped because the slot was not clear at launch) or that are not clear now
+ * (with no launch in flight every slot must be zero), and resets them, so the
+ * next launch on them is whole.  *faults = 0: no fault.  Call it outside graph
+ * capture and with no launch of this library being issued from another host
+ * thread.  The reference has no such state (its SDPA has no persistent
+ * launches); this is the check behind the Python layer's check mode
+ * (LH_CHECK_INDICES=1).
+ */
+int lh_attn_status(int *faults);
+
+/*
+ * Diagnostics: the device address of the counter slot (32 unsigned words) that
+ * persistent launches on `stream` use on the current device, assigned on first
+ * use; LH_ERR_UNSUPPORTED when every slot is taken.  Tests use it to plant a
+ * dirty slot.  No counterpart in the reference.
+ */
+int lh_attn_queue_slot(void *stream, void **slot);
 
 /*
  * Fan-out of each selected row onto the base positions it stands for:

@@ -52,6 +52,8 @@ _SIGS = {
                               _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P]),
     "lh_attn_bwd_dq": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _I, _P,
                             _I, _I, _I, _I, _F, _P, _P, _P, _P, _P]),
+    "lh_attn_status": (_I, [_P]),
+    "lh_attn_queue_slot": (_I, [_P, _P]),
     "lh_scatter_fwd": (_I, [_P, _P, _P, _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_scatter_bwd": (_I, [_P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_pyramid_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
@@ -283,6 +285,7 @@ def dilated_scores(xq, xk, xv, dilation: int, S_tot: int, scale: float | None = 
         rc = lib().lh_dilated_scores(_ptr(xq), _ptr(xk), _ptr(xv), _ptr(sqk), _ptr(skq), B, S, H, D, dilation,
                                      S_tot, float(scale or 0.0), _stream(dev))
     _check(rc, "lh_dilated_scores")
+    _check_queues(dev, "lh_dilated_scores")
     return sqk, skq
 
 
@@ -357,6 +360,28 @@ def build_inverse(indices, S_tot: int, validate: bool = False):
     return inv
 
 
+def attn_status(device=None) -> int:
+    """Work-queue faults of the persistent attention launches on ``device``
+    since the last call: 0 when every launch's blocks added up, else the number
+    of counter slots found not cleared at launch (blocks skipped or repeated),
+    which are reset.  Synchronizes the device."""
+    f = ctypes.c_int(0)
+    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
+        rc = lib().lh_attn_status(ctypes.byref(f))
+    _check(rc, "lh_attn_status")
+    return f.value
+
+
+def _check_queues(dev, what: str):
+    """In check mode, raise if an attention launch found its work-queue counters dirty."""
+    if _check_indices:
+        n = attn_status(dev)
+        if n:
+            raise LighthouseHipError(
+                f"{what}: {n} work-queue counter slot(s) were not cleared at launch, so blocks were skipped "
+                "or repeated and the outputs are not to be trusted; the slots are reset now")
+
+
 class Rows:
     """Where row r of (b, h) lives: ``base`` [.., r, .., D] for r < split,
     else ``pool`` at r - split.  Strides are in elements, D contiguous."""
@@ -404,6 +429,7 @@ def attn_fwd(rows: Rows, indices, B: int, H: int, n: int, D: int = D_SUPPORTED, 
     with torch.cuda.device(dev):
         rc = lib().lh_attn_fwd(*rows.args(), _ptr(idx), B, H, n, D, scale, _ptr(out), _ptr(lse), _stream(dev))
     _check(rc, "lh_attn_fwd")
+    _check_queues(dev, "lh_attn_fwd")
     return out, lse
 
 
@@ -419,6 +445,7 @@ def attn_bwd_dkdv(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta,
         rc = lib().lh_attn_bwd_dkdv(*rows.args(), _ptr(idx), B, H, n, D, scale, _ptr(dout.contiguous()),
                                     _ptr(lse), _ptr(delta), _ptr(dk), _ptr(dv), _stream(dev))
     _check(rc, "lh_attn_bwd_dkdv")
+    _check_queues(dev, "lh_attn_bwd_dkdv")
     return dk, dv
 
 
@@ -434,6 +461,7 @@ def attn_bwd_dq(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D
         rc = lib().lh_attn_bwd_dq(*rows.args(), _ptr(idx), B, H, n, D, scale, _ptr(dout.contiguous()),
                                   _ptr(lse), _ptr(delta), _ptr(dq), _stream(dev))
     _check(rc, "lh_attn_bwd_dq")
+    _check_queues(dev, "lh_attn_bwd_dq")
     return dq
 
 
@@ -450,6 +478,7 @@ def attn_bwd(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D: i
         rc = lib().lh_attn_bwd(*rows.args(), _ptr(idx), B, H, n, D, scale, _ptr(dout), _ptr(lse), _ptr(delta),
                                _ptr(dq), _ptr(dk), _ptr(dv), _stream(dev))
     _check(rc, "lh_attn_bwd")
+    _check_queues(dev, "lh_attn_bwd")
     return dq, dk, dv
 
 

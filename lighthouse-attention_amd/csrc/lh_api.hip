@@ -8,8 +8,9 @@ extern "C" const char* lh_strerror(int rc) {
     case LH_ERR_DOMAIN: return "geometry outside the reference selection kernel's domain (strict mode)";
     case LH_ERR_LAUNCH: return "HIP kernel launch failed";
     case LH_ERR_UNSUPPORTED: return "shape beyond this build's limits";
+    case LH_ERR_RUNTIME: return "a HIP runtime call failed";
     default: return "unknown error";
   }
 }
 
-extern "C" int lh_abi_version(void) { return 5; }
+extern "C" int lh_abi_version(void) { return LH_ABI_VERSION; }

@@ -203,11 +203,19 @@ __device__ __forceinline__ bool plan_next(const QPlan& p, int bin, int k, int& q
 // workgroup runs a block does not change its result: every block is computed
 // whole by one workgroup.
 struct WorkQ {
-  // counters of this launch (nullptr = plain grid): [0, 8) queue heads,
-  // [8] workgroups done, [9] mask of drained queues
+  // counters of this launch (nullptr = plain grid), a slot of WQ_STRIDE words:
+  // [0, 8) queue heads, [8] mask of drained queues, [10, 12) the done word
+  // (64-bit: workgroups finished in the low half, blocks they ran in the high
+  // half), [12] fault flag (sticky: the launches never clear it)
   unsigned* ctr;
   int slots;  // workgroups per queue (grid / 8); their first blocks are not counted
 };
+constexpr int WQ_DRAINED = 8, WQ_DONE = 10, WQ_FAULT = 12, WQ_CLEAR = 12;
+
+// Set (bit 0) by a persistent launch whose blocks did not add up to its block
+// count, i.e. that found its counters not cleared at launch (lh_attn_status
+// reads and resets it with the slots that flagged).
+__device__ unsigned g_wq_fault;
 
 // first (b, h) of queue x; queue x holds [wq_lo(x), wq_lo(x + 1))
 __device__ __forceinline__ int wq_lo(int x, int BH) { return (int)(((long long)x * BH) >> 3); }
@@ -232,6 +240,21 @@ __device__ __forceinline__ bool wq_first(const WorkQ& q, int nblk, int BH, bool 
   return true;
 }
 
+// The counter address as a per-lane (VGPR) value.  Every work-queue atomic is
+// made by one lane, and with a per-lane address the compiler's atomic
+// optimizer leaves it alone: for a uniform address it would read the result at
+// once, or, for a value it cannot prove uniform, scan the active lanes in a
+// loop that addresses lanes through M0 (which the direct loads' inline
+// assembly assumes no compiler instruction touches).
+__device__ __forceinline__ unsigned* lane_addr(unsigned* p) {
+  int zero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+  return p + zero;
+}
+__device__ __forceinline__ unsigned long long* lane_addr64(unsigned* p) {
+  return reinterpret_cast<unsigned long long*>(lane_addr(p));
+}
+
 // Thread 0, shortly before its workgroup's block ends: reserve the next entry
 // of the workgroup's own queue.  Returns the counter's old value c (the entry
 // is slots + c, valid while below the queue's length), or -1 when the queue has
@@ -242,18 +265,29 @@ __device__ __forceinline__ bool wq_first(const WorkQ& q, int nblk, int BH, bool 
 __device__ __forceinline__ int wq_reserve(const WorkQ& q, int nblk, int BH) {
   const int x = blockIdx.x & 7;
   if (wq_len(x, nblk, BH) <= q.slots) return -1;
-  int zero;
-  asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
-  return (int)atomicAdd(q.ctr + x + zero, 1u);
+  return (int)atomicAdd(lane_addr(q.ctr + x), 1u);
 }
 
 // Next block of this workgroup (persistent launches; false: none left), from
 // thread 0's reservation (wq_reserve's value; -1: none made) or by taking
 // entries itself.  Every thread calls it once the previous block's LDS reads
-// are done; s is two ints of LDS.  The previous block's direct-to-LDS loads are
-// waited for here.
-__device__ __forceinline__ bool wq_next(const WorkQ& q, int nblk, int BH, bool heavy_last, int reserved, int& bh,
-                                        int& blk, int* s) {
+// are done, with nrun the number of blocks the workgroup has run; s is two
+// ints of LDS.  The previous block's direct-to-LDS loads are waited for here.
+//
+// A workgroup that finds no block left adds itself and its block count to the
+// done word.  The one that completes the workgroup count checks that the blocks
+// add up to the launch's (nblk * BH; fewer when a queue head was not zero at
+// launch, so entries were skipped) and returns the counters to zero.  A
+// mismatch, or a workgroup count already past the grid, sets the slot's fault
+// flag and g_wq_fault.  With the done word itself not zero at launch, an
+// earlier workgroup believes it is the last and clears the counters while
+// others still run; those then sweep the queues again, which repeats blocks
+// (same arithmetic, same values) but skips none, and leave the slot not clear,
+// which lh_attn_status finds once the device is idle.  A dirty drained mask
+// only keeps other XCDs from entries that their owners still take.  No path
+// waits on another workgroup, so a dirty slot cannot hang a launch.
+__device__ __forceinline__ bool wq_next(const WorkQ& q, int nblk, int BH, bool heavy_last, int reserved, int nrun,
+                                        int& bh, int& blk, int* s) {
   if (threadIdx.x == 0) {
     const int x0 = blockIdx.x & 7;
     int found = -1, fx = x0;
@@ -263,29 +297,39 @@ __device__ __forceinline__ bool wq_next(const WorkQ& q, int nblk, int BH, bool h
       if (q.slots + reserved < wq_len(x0, nblk, BH))
         found = q.slots + reserved;
       else
-        drained = atomicOr(q.ctr + 9, 1u << x0);
+        drained = atomicOr(lane_addr(q.ctr + WQ_DRAINED), 1u << x0);
       d = 1;
     }
     for (; d < 8 && found < 0; ++d) {
       const int x = (x0 + d) & 7;
       const int len = wq_len(x, nblk, BH);
       if (len <= q.slots || ((drained >> x) & 1)) {
-        if (d == 0) drained = atomicOr(q.ctr + 9, 0u);  // no counted entries here: learn which queues are drained
+        if (d == 0) drained = atomicOr(lane_addr(q.ctr + WQ_DRAINED), 0u);  // no counted entries here: learn which queues are drained
         continue;
       }
-      const int j = q.slots + (int)atomicAdd(q.ctr + x, 1u);
+      const int j = q.slots + (int)atomicAdd(lane_addr(q.ctr + x), 1u);
       if (j < len) {
         found = j;
         fx = x;
       } else if (d == 0) {  // own queue drained: mark it, and learn which others are
-        drained = atomicOr(q.ctr + 9, 1u << x);
+        drained = atomicOr(lane_addr(q.ctr + WQ_DRAINED), 1u << x);
       } else {
-        atomicOr(q.ctr + 9, 1u << x);
+        atomicOr(lane_addr(q.ctr + WQ_DRAINED), 1u << x);
       }
     }
-    if (found < 0 && atomicAdd(q.ctr + 8, 1u) == gridDim.x - 1) {
+    if (found < 0) {
+      const unsigned long long old =
+          atomicAdd(lane_addr64(q.ctr + WQ_DONE), 1ull | ((unsigned long long)(unsigned)nrun << 32));
+      const unsigned wg = (unsigned)old;
+      if (wg >= gridDim.x ||
+          (wg == gridDim.x - 1 && (unsigned)(old >> 32) + (unsigned)nrun != (unsigned)nblk * (unsigned)BH)) {
+        atomicOr(lane_addr(q.ctr + WQ_FAULT), 1u);
+        atomicOr(lane_addr(&g_wq_fault), 1u);
+      }
+      if (wg == gridDim.x - 1) {
 #pragma unroll
-      for (int i = 0; i < 10; ++i) atomicExch(q.ctr + i, 0u);
+        for (int i = 0; i < WQ_CLEAR; ++i) atomicExch(lane_addr(q.ctr + i), 0u);
+      }
     }
     s[0] = found;
     s[1] = fx;
@@ -667,7 +711,7 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArg
     have = qb != PLAN_NONE;
   } else {
     have = wq_first(q, a.nq, a.BH, true, bh, qb);
-    if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, true, -1, bh, qb, wq_s);
+    if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, true, -1, 0, bh, qb, wq_s);
   }
   for (int k = 1; have; ++k) {
     fwd_block<EPI>(a, bh, qb, K0, K1, V0, V1);
@@ -675,14 +719,14 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArg
     if (p.bph)
       have = plan_next(p, bin, k, qb);
     else
-      have = q.ctr && wq_next(q, a.nq, a.BH, true, -1, bh, qb, wq_s);
+      have = q.ctr && wq_next(q, a.nq, a.BH, true, -1, k, bh, qb, wq_s);
   }
 }
 
 // ===========================================================================
 // backward dQ (query-stationary)
 // ===========================================================================
-__device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], const u32x4 (&qf)[8], const u32x4 (&df)[8],
+__device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], float& rsum, const u32x4 (&qf)[8], const u32x4 (&df)[8],
                                         const bf16_t* Ks, const bf16_t* Vs, int k0, int my_q, int n, int lane,
                                         float sl2, float nlse, float dlt, bool mask) {
   const int hh = lane >> 5;
@@ -726,6 +770,18 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], const u32x4 (&qf)[8]
 #pragma unroll
     for (int v = 0; v < 16; ++v) s[v] = ex2(fmaf(s[v], sl2, nlse)) * dp[v];
     const u32x4 f0 = pack_frag(s, 0), f1 = pack_frag(s, 1);
+    {
+      // this lane's share of the row sum of the bf16 dS that the product below uses
+      const bf16x2 one = as_bf2(0x3f803f80u);
+      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.x), one, rsum, false);
+      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.y), one, rsum, false);
+      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.z), one, rsum, false);
+      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.w), one, rsum, false);
+      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.x), one, rsum, false);
+      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.y), one, rsum, false);
+      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.z), one, rsum, false);
+      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.w), one, rsum, false);
+    }
     __builtin_amdgcn_s_setprio(1);
     {
       // operand i: column block i & 3, key rows kb * 32 + 16 (i >> 2)
@@ -747,8 +803,21 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], const u32x4 (&qf)[8]
 }
 
 // dQ of one query block qb of (b, h) bh.
+//
+// Key centring.  dQ_i = scale sum_t dS_it k_t, and sum_t dS_it = 0 on every
+// row (dS = P (dP - delta), delta = sum_t P dP), so dQ_i = scale sum_t dS_it
+// (k_t - c) for any vector c.  The product takes dS rounded to bf16, whose
+// errors (and those of delta, formed from the bf16 O) multiply k_t: with a
+// large component that the keys share (a channel constant over the keys, as
+// trained models' keys often have), that product alone errs far beyond the
+// bf16 tolerance.  The kernel therefore also sums r_i = sum_t bf16(dS_it) (the
+// same bf16 values, by v_dot2 against ones) and subtracts scale r_i c at the
+// end, which gives scale sum_t bf16(dS_it) (k_t - c): the rounding errors then
+// multiply k_t - c instead of k_t.  c is the fp32 mean of 64 key rows spread
+// evenly over the block's causal key range, read with plain loads beside the
+// first tile's direct loads (kc: 128 + 8 x 128 floats of LDS).
 __device__ __forceinline__ void dq_block(const AttnArgs& a, int bh, int qb, bf16_t* K0, bf16_t* K1, bf16_t* V0,
-                                         bf16_t* V1) {
+                                         bf16_t* V1, float* kc) {
   constexpr int BM = 32 * QW;
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -762,7 +831,11 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, int bh, int qb, bf16
     bool pooled;
     const uint32_t o = row_off(m, my_q, pooled) + 8 * hh;
     const bf16_t* p = (pooled ? m.qp : m.q) + o;
-    const bf16_t* pd = a.dout + ((int64_t)bh * n + qc) * LH_D + 8 * hh;
+    // formed from opaque copies so that the compiler does not hoist per-lane
+    // address parts out of the persistent block loop (they would spill)
+    int row = qc, half = hh;
+    asm volatile("" : "+v"(row), "+v"(half));
+    const bf16_t* pd = a.dout + ((int64_t)bh * n + row) * LH_D + 8 * half;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       qf[c] = ldg16(p + 16 * c);
@@ -778,19 +851,59 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, int bh, int qb, bf16
   load_rows<QW>(rr, m, 0, wave, lane);
   issue_rows<QW>(K0, m.k, m.kp, V0, m.v, m.vp, m, rr, wave, lane);
   load_rows<QW>(rr, m, BN, wave, lane);
+  // key sample for the centre: thread t reads 16 bytes (dims 8 (t % 16) ..) of
+  // sample rows t / 16 and t / 16 + 32, sample s at key (s kend) / 64
+  u32x4 ks0, ks1;
+  {
+    const int ch = tid & 15, s0 = tid >> 4;
+    bool pooled;
+    uint32_t o = row_off(m, (s0 * kend) >> 6, pooled);
+    ks0 = ldg16((pooled ? m.kp : m.k) + o + 8 * ch);
+    o = row_off(m, ((s0 + 32) * kend) >> 6, pooled);
+    ks1 = ldg16((pooled ? m.kp : m.k) + o + 8 * ch);
+  }
   wait_loads();
+  {
+    // sum the two rows, then over the four lanes of this wave that hold the
+    // same 8 dims, then over the waves in LDS
+    float c8[8];
+    const uint32_t w0[4] = {ks0.x, ks0.y, ks0.z, ks0.w}, w1[4] = {ks1.x, ks1.y, ks1.z, ks1.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      c8[2 * e] = __uint_as_float(w0[e] << 16) + __uint_as_float(w1[e] << 16);
+      c8[2 * e + 1] = __uint_as_float(w0[e] & 0xffff0000u) + __uint_as_float(w1[e] & 0xffff0000u);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      c8[e] += __shfl_xor(c8[e], 16);
+      c8[e] += __shfl_xor(c8[e], 32);
+    }
+    if (lane < 16) {
+      float4* dst = reinterpret_cast<float4*>(kc + 128 + wave * 128 + 8 * lane);
+      dst[0] = float4{c8[0], c8[1], c8[2], c8[3]};
+      dst[1] = float4{c8[4], c8[5], c8[6], c8[7]};
+    }
+  }
   __syncthreads();
+  if (tid < 128) {
+    float c = 0.f;
+#pragma unroll
+    for (int w = 0; w < QW; ++w) c += kc[128 + w * 128 + tid];
+    kc[tid] = c * (1.0f / 64.0f);  // read in the epilogue, past the step loop's barriers
+  }
 
   floatx16 acc[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) acc[d] = floatx16{};
+  float rsum = 0.f;
   const int nfull = min((qw + 1) / BN, n / BN);
 
   auto step = [&](int j, const bf16_t* Ks, const bf16_t* Vs, bf16_t* Kn, bf16_t* Vn) {
     const int k0 = j * BN;
     if (j + 1 < nt) issue_rows<QW>(Kn, m.k, m.kp, Vn, m.v, m.vp, m, rr, wave, lane);
     if (j + 2 < nt) load_rows<QW>(rr, m, k0 + 2 * BN, wave, lane);
-    if (j < nt && k0 <= qw + 31) dq_tile(acc, qf, df, Ks, Vs, k0, my_q, n, lane, a.sl2, nlse, dlt, j >= nfull);
+    if (j < nt && k0 <= qw + 31)
+      dq_tile(acc, rsum, qf, df, Ks, Vs, k0, my_q, n, lane, a.sl2, nlse, dlt, j >= nfull);
     wait_loads();
     __syncthreads();
   };
@@ -799,8 +912,25 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, int bh, int qb, bf16
     step(j + 1, K1, V1, K0, V0);
   }
 
+  // the two lane halves hold the two halves of each row's keys
+  rsum += __shfl_xor(rsum, 32);
   if (my_q >= n) return;
-  store_rows_bf16(a.dq + ((int64_t)bh * n + my_q) * LH_D, acc, a.scale, hh);
+  // acc[d][4 g + e] is dim 32 d + 8 g + 4 hh + e
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 c = *reinterpret_cast<const float4*>(kc + 32 * d + 8 * g + 4 * hh);
+      acc[d][4 * g + 0] = fmaf(-rsum, c.x, acc[d][4 * g + 0]);
+      acc[d][4 * g + 1] = fmaf(-rsum, c.y, acc[d][4 * g + 1]);
+      acc[d][4 * g + 2] = fmaf(-rsum, c.z, acc[d][4 * g + 2]);
+      acc[d][4 * g + 3] = fmaf(-rsum, c.w, acc[d][4 * g + 3]);
+    }
+  {
+    int row = my_q, half = hh;
+    asm volatile("" : "+v"(row), "+v"(half));
+    store_rows_bf16(a.dq + ((int64_t)bh * n + row) * LH_D, acc, a.scale, half);
+  }
 }
 
 __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const AttnArgs a, const QPlan p, const WorkQ q) {
@@ -808,6 +938,7 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const Attn
   __shared__ __attribute__((aligned(1024))) bf16_t K1[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t V0[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t V1[TILE];
+  __shared__ __attribute__((aligned(16))) float KC[128 + QW * 128];  // key centre + per-wave partial sums
   __shared__ int wq_s[2];
   int bh, qb, bin = 0;
   bool have;
@@ -816,15 +947,15 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const Attn
     have = qb != PLAN_NONE;
   } else {
     have = wq_first(q, a.nq, a.BH, true, bh, qb);
-    if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, true, -1, bh, qb, wq_s);
+    if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, true, -1, 0, bh, qb, wq_s);
   }
   for (int k = 1; have; ++k) {
-    dq_block(a, bh, qb, K0, K1, V0, V1);
+    dq_block(a, bh, qb, K0, K1, V0, V1, KC);
     // the next block starts after this one's last tile reads
     if (p.bph)
       have = plan_next(p, bin, k, qb);
     else
-      have = q.ctr && wq_next(q, a.nq, a.BH, true, -1, bh, qb, wq_s);
+      have = q.ctr && wq_next(q, a.nq, a.BH, true, -1, k, bh, qb, wq_s);
   }
 }
 
@@ -1032,7 +1163,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
   const LaneLds ll = lane_lds(lane);
   int bh, kblk;
   bool have = wq_first(q, a.nq, a.BH, false, bh, kblk);  // early key blocks see the most queries
-  if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, false, -1, bh, kblk, wq_s);
+  if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, false, -1, 0, bh, kblk, wq_s);
+  int nrun = 0;  // blocks this workgroup has run
   while (have) {
     // wave-uniform by construction; said explicitly, or the compiler keeps bh * n (and the
     // addresses derived from it) in vector registers and spills them across the loop
@@ -1224,7 +1356,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
         store_rows_bf16(a.dk + ((int64_t)bh * n + row) * LH_D, acc, a.scale, half);
     }
     if (!q.ctr) break;
-    have = wq_next(q, a.nq, a.BH, false, next, bh, kblk, wq_s);  // the previous block's copies are waited for there
+    have = wq_next(q, a.nq, a.BH, false, next, ++nrun, bh, kblk, wq_s);  // the previous block's copies are waited for there
   }
 }
 
@@ -1703,33 +1835,62 @@ int make_plan(int BH, int n, QPlan& p) {
 // Work-queue counters of the persistent launches: one 128-byte slot per
 // (device, stream), so launches that may run at the same time (different
 // streams) never share counters, while launches on one stream run one after
-// the other and each leaves its slot cleared.  A launch captured into a graph
-// keeps the slot of the stream it was captured on.  Past WQ_SLOTS streams on a
-// device, launches fall back to the plain grid.
-constexpr int WQ_SLOTS = 64, WQ_STRIDE = 32;
+// the other and each leaves its slot cleared.  A launch made while its stream
+// is being captured into a graph gets a slot of its own that no other launch
+// uses (graphs captured one after the other on one stream can be replayed on
+// different streams at once; only a graph replayed beside itself races).  Past
+// WQ_SLOTS slots on a device, launches fall back to the plain grid.
+constexpr int WQ_SLOTS = 1024, WQ_STRIDE = 32;
 __device__ __attribute__((aligned(256))) unsigned g_wq[WQ_SLOTS * WQ_STRIDE];
 
-unsigned* wq_counters(hipStream_t st) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+struct WqDevice {
+  unsigned* base = nullptr;  // device address of g_wq (hipGetSymbolAddress)
+  unsigned* fault = nullptr;  // device address of g_wq_fault
+  int used = 0;
+};
+
+std::mutex& wq_mutex() {
   static std::mutex mu;
-  static unsigned* base[64];
-  static int used[64];
-  static std::map<std::pair<int, std::pair<uintptr_t, std::thread::id>>, int> slot;
-  std::lock_guard<std::mutex> g(mu);
-  if (!base[dev]) {
+  return mu;
+}
+
+// the current device's slot array (caller holds wq_mutex); nullptr when unavailable
+WqDevice* wq_device(int& dev) {
+  static WqDevice devs[64];
+  dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  WqDevice& d = devs[dev];
+  if (!d.base) {
     void* ptr = nullptr;
+    void* fptr = nullptr;
     if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_wq)) != hipSuccess || !ptr) return nullptr;
-    base[dev] = static_cast<unsigned*>(ptr);
+    if (hipGetSymbolAddress(&fptr, HIP_SYMBOL(g_wq_fault)) != hipSuccess || !fptr) return nullptr;
+    d.base = static_cast<unsigned*>(ptr);
+    d.fault = static_cast<unsigned*>(fptr);
   }
+  return &d;
+}
+
+unsigned* wq_counters(hipStream_t st) {
+  std::lock_guard<std::mutex> g(wq_mutex());
+  int dev = 0;
+  WqDevice* d = wq_device(dev);
+  if (!d) return nullptr;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) return nullptr;
+  if (cs != hipStreamCaptureStatusNone) {  // a captured launch: a slot of its own
+    if (d->used == WQ_SLOTS) return nullptr;
+    return d->base + (d->used++) * WQ_STRIDE;
+  }
+  static std::map<std::pair<int, std::pair<uintptr_t, std::thread::id>>, int> slot;
   // hipStreamPerThread names a different stream on every host thread
   const std::thread::id tid = st == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
   const auto key = std::make_pair(dev, std::make_pair(reinterpret_cast<uintptr_t>(st), tid));
   auto it = slot.find(key);
-  if (it != slot.end()) return base[dev] + it->second * WQ_STRIDE;
-  if (used[dev] == WQ_SLOTS) return nullptr;
-  slot[key] = used[dev];
-  return base[dev] + (used[dev]++) * WQ_STRIDE;
+  if (it != slot.end()) return d->base + it->second * WQ_STRIDE;
+  if (d->used == WQ_SLOTS) return nullptr;
+  slot[key] = d->used;
+  return d->base + (d->used++) * WQ_STRIDE;
 }
 
 // Grid of a launch over BH (b, h) of nblk blocks each: one workgroup per CU
@@ -1842,6 +2003,46 @@ extern "C" int lh_attn_bwd_dq(const void* q, const void* k, const void* v, int64
                         lse, delta, dq, nullptr, nullptr, stream);
 }
 
+extern "C" int lh_attn_status(int* faults) {
+  if (!faults) return LH_ERR_INVALID_ARG;
+  *faults = 0;
+  std::lock_guard<std::mutex> g(wq_mutex());
+  int dev = 0;
+  WqDevice* d = wq_device(dev);
+  if (!d) return LH_ERR_RUNTIME;
+  // With the device idle no launch is in flight, so every slot's counters must
+  // be zero: a slot is faulty when a launch flagged it or when it is not clear.
+  if (hipDeviceSynchronize() != hipSuccess) return LH_ERR_RUNTIME;
+  std::vector<unsigned> w((size_t)WQ_SLOTS * WQ_STRIDE);
+  if (hipMemcpy(w.data(), d->base, w.size() * sizeof(unsigned), hipMemcpyDeviceToHost) != hipSuccess)
+    return LH_ERR_RUNTIME;
+  unsigned flag = 0;
+  if (hipMemcpy(&flag, d->fault, sizeof(flag), hipMemcpyDeviceToHost) != hipSuccess) return LH_ERR_RUNTIME;
+  int n = 0;
+  for (int i = 0; i < WQ_SLOTS; ++i) {
+    unsigned* c = w.data() + (size_t)i * WQ_STRIDE;
+    if (std::all_of(c, c + WQ_STRIDE, [](unsigned x) { return x == 0u; })) continue;
+    ++n;
+    std::fill(c, c + WQ_STRIDE, 0u);
+    if (hipMemcpy(d->base + (size_t)i * WQ_STRIDE, c, WQ_STRIDE * sizeof(unsigned), hipMemcpyHostToDevice) !=
+        hipSuccess)
+      return LH_ERR_RUNTIME;
+  }
+  if (flag) {
+    flag = 0;
+    if (hipMemcpy(d->fault, &flag, sizeof(flag), hipMemcpyHostToDevice) != hipSuccess) return LH_ERR_RUNTIME;
+    if (!n) n = 1;
+  }
+  *faults = n;
+  return LH_OK;
+}
+
+extern "C" int lh_attn_queue_slot(void* stream, void** slot) {
+  if (!slot) return LH_ERR_INVALID_ARG;
+  *slot = wq_counters(reinterpret_cast<hipStream_t>(stream));
+  return *slot ? LH_OK : LH_ERR_UNSUPPORTED;
+}
+
 extern "C" int lh_dilated_scores(const void* xq, const void* xk, const void* xv, float* scores_qk, float* scores_kq,
                                  int B, int S, int H, int D, int dilation, int S_tot, float scale, void* stream) {
   if (D != LH_D) return LH_ERR_UNSUPPORTED;
@@ -1870,18 +2071,22 @@ extern "C" int lh_dilated_scores(const void* xq, const void* xk, const void* xv,
 }
 
 namespace {
-// Segments of the GLA walk: enough to give every CU a workgroup (one per CU:
-// the scoring kernel holds 139 KB of LDS), at least 8 chunks each.  segments > 0
-// asks for that many (clamped to the chunk count).  Every segment is non-empty.
+// Segments of the GLA walk.  Automatic: one per GLA_CHUNKS_PER_SEGMENT chunks
+// of 64 tokens (at least one), from the sequence length alone, so that a
+// sequence's walk, and with it the last bits of its bf16 scores, never depends
+// on how many sequences share the launch (B, dilation, H) or on the device.
+// At the reference's GLA flavor (32768 tokens, dilation 4: 128 chunks) that is
+// 4 segments, 256 workgroups for 8 heads (one per CU: the scoring kernel holds
+// 139 KB of LDS).  segments > 0 asks for that many (clamped to the chunk
+// count).  Every segment is non-empty.
+constexpr int GLA_CHUNKS_PER_SEGMENT = 32;
 void gla_segments(int B, int S, int H, int dilation, int segments, int* P, int* cps) {
+  (void)B;
+  (void)H;
   const int T = S / dilation;
   const int nch = (T + 63) / 64;
-  const long long units = (long long)B * dilation * H * 2;
   long long want = segments;
-  if (want <= 0) {
-    want = units >= 256 ? 1 : 256 / units;
-    want = std::min<long long>(want, std::max(1, nch / 8));
-  }
+  if (want <= 0) want = std::max(1, nch / GLA_CHUNKS_PER_SEGMENT);
   want = std::max<long long>(1, std::min<long long>(want, nch));
   *cps = (int)((nch + want - 1) / want);
   *P = (nch + *cps - 1) / *cps;

@@ -37,7 +37,15 @@ def test_library_exports_every_declared_symbol(pkg):
     for n in _declared():
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
     assert set(_declared()) == set(pkg._native.EXPORTED)
-    assert lib.lh_abi_version() == 5
+
+
+def test_abi_version_matches_header(pkg):
+    """The header's LH_ABI_VERSION is what the built library reports, so a C
+    caller can compare the two at start-up."""
+    with open(HEADER) as f:
+        m = re.search(r"#define\s+LH_ABI_VERSION\s+(\d+)", f.read())
+    assert m, "LH_ABI_VERSION is not defined in the header"
+    assert pkg._native.lib().lh_abi_version() == int(m.group(1))
 
 
 def test_gla_workspace_geometry(pkg):
@@ -50,8 +58,9 @@ def test_gla_workspace_geometry(pkg):
     assert f(1, 32768, 8, 128, 4, 1) == 0
     assert f(1, 32768, 8, 128, 4, 6) == units * 5 * (128 * 128 + 1) * 4  # 128 chunks: 22 per segment, 6 segments
     assert f(1, 32768, 8, 128, 4, 100000) == units * 127 * (128 * 128 + 1) * 4  # clamped to one chunk each
-    assert f(1, 1024, 2, 128, 4, 0) == 0  # 4 chunks: fewer than 8 per segment, one walk
-    assert f(64, 32768, 8, 128, 4, 0) == 0  # 4096 workgroups already
+    assert f(1, 1024, 2, 128, 4, 0) == 0  # 4 chunks: one walk
+    assert f(1, 8188 * 4, 2, 128, 4, 0) == (1 * 4 * 2 * 2) * 3 * (128 * 128 + 1) * 4  # 128 chunks, last ragged: 4
+    assert f(64, 32768, 8, 128, 4, 0) == 64 * units * 3 * (128 * 128 + 1) * 4  # per-sequence rule: 4 segments
     assert f(1, 1000, 1, 128, 3, 0) == -1  # S not a multiple of the dilation
     assert f(1, 1024, 1, 64, 4, 0) == -1  # D != 128
     assert f(0, 1024, 1, 128, 4, 0) == -1
@@ -59,8 +68,8 @@ def test_gla_workspace_geometry(pkg):
 
 def test_strerror(pkg):
     lib = pkg._native.lib()
-    for rc in range(5):
-        assert lib.lh_strerror(rc)
+    for rc in range(6):
+        assert b"unknown" not in lib.lh_strerror(rc)
     assert b"unknown" in lib.lh_strerror(99)
 
 

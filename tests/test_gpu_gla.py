@@ -164,3 +164,22 @@ def test_gla_workspace_errors(pkg, dev):
     assert lib.lh_gla_scores(*args, ptr(ws), need - 4, N._stream(dev)) == 1  # LH_ERR_INVALID_ARG
     assert lib.lh_gla_scores(*args, ptr(ws), need, N._stream(dev)) == 0
     torch.cuda.synchronize()
+
+
+def test_gla_scores_independent_of_batch(pkg, dev):
+    """A sequence's scores are bit-identical whether it is scored alone or as one
+    of several sequences and heads: the automatic segment count depends on the
+    per-sequence length only (here 4 segments of 32 chunks)."""
+    N = pkg._native
+    B, S, H, dil, L, p = 3, 32768, 2, 4, 3, 4
+    print(f"gla batch independence B={B} S={S} H={H} dil={dil}", flush=True)
+    xs, gk, xd, gd = _inputs(B, S, H, "typical", 11, dev)
+    _, _, S_tot = N.pyramid_lengths(S, L, p)
+    assert N.lib().lh_gla_workspace_bytes(B, S, H, D, dil, 0) == B * dil * H * 2 * 3 * (D * D + 1) * 4
+    full = N.gla_scores(*xd, gd, dil, S_tot)
+    for b in (0, 2):
+        for h in range(H):
+            one = N.gla_scores(*[x[b:b + 1, :, h:h + 1].contiguous() for x in xd],
+                               gd[b:b + 1, :, h:h + 1].contiguous(), dil, S_tot)
+            for f_, o_, name in zip(full, one, ("qk", "kq")):
+                assert torch.equal(f_[b:b + 1, h:h + 1, :S], o_[..., :S]), f"batch {b} head {h} {name} differs"

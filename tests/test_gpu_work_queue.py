@@ -163,3 +163,138 @@ def test_queue_graph_replay(pkg, dev):
         for name, x, y in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
             assert torch.equal(x, y), f"replay {r}: {name} differs from the eager result"
         assert torch.equal(eager[0], ref[0]), f"replay {r}: eager o differs"
+
+
+def _hip_memcpy():
+    """hipMemcpy of the HIP runtime torch has loaded (the library binds the same one)."""
+    import ctypes
+    h = ctypes.CDLL("libamdhip64.so.7")
+    f = h.hipMemcpy
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    return f
+
+
+def _slot(pkg, dev):
+    import ctypes
+    p = ctypes.c_void_p()
+    rc = pkg._native.lib().lh_attn_queue_slot(ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream),
+                                              ctypes.byref(p))
+    assert rc == 0 and p.value
+    return p.value
+
+
+def _slot_words(pkg, dev):
+    import ctypes
+    buf = (ctypes.c_uint32 * 32)()
+    torch.cuda.synchronize(dev)
+    assert _hip_memcpy()(ctypes.cast(buf, ctypes.c_void_p), ctypes.c_void_p(_slot(pkg, dev)), 128, 2) == 0
+    return list(buf)
+
+
+def _plant(pkg, dev, word, value):
+    import ctypes
+    buf = (ctypes.c_uint32 * 1)(value)
+    torch.cuda.synchronize(dev)
+    assert _hip_memcpy()(ctypes.c_void_p(_slot(pkg, dev) + 4 * word), ctypes.cast(buf, ctypes.c_void_p), 4, 1) == 0
+
+
+# (word, value, flagged, outputs whole): a queue head past zero skips entries
+# (blocks missing: flagged); a drained mask only stops other XCDs from taking
+# entries their owners still take (outputs whole, nothing to flag); a done word
+# not zero makes an early workgroup clear the counters while others run, and
+# they sweep the queues again (outputs whole, flagged); the done word's block
+# count off (flagged).  For B = 1, H = 3, queues 2, 5 and 7 hold one head each.
+DIRT = [(2, 3, True, False), (8, (1 << 2) | (1 << 5), False, True), (10, 5, True, True), (11, 7, True, True)]
+
+
+@pytest.mark.parametrize("word,value,flagged,whole", DIRT)
+@pytest.mark.parametrize("kernel", ["fwd", "dkdv"])
+def test_queue_dirty_slot_detected(pkg, dev, kernel, word, value, flagged, whole):
+    """A counter slot planted not clear before a persistent launch: the launch's
+    block count says so (lh_attn_status > 0, and check mode raises), the slot
+    comes back cleared, and the next launch is bit-equal to a clean one."""
+    n, B, H = 30000, 1, 3
+    print(f"dirty slot kernel={kernel} word={word} value={value:#x}", flush=True)
+    N = pkg._native
+    xs = [_rand((B, n, H, 128), 110 + i, dev) for i in range(3)]
+    rows = N.Rows(*xs, (xs[0].stride(0), xs[0].stride(1), xs[0].stride(2)))
+    o, lse = N.attn_fwd(rows, None, B, H, n)
+    do = _rand((B, H, n, 128), 115, dev)
+    delta = (do.float() * o.float()).sum(-1)
+
+    def run():
+        if kernel == "fwd":
+            return N.attn_fwd(rows, None, B, H, n)
+        return N.attn_bwd_dkdv(rows, None, B, H, n, do, lse, delta)
+
+    ref = run()
+    assert N.attn_status(dev) == 0, "a clean launch was flagged"
+    assert not any(_slot_words(pkg, dev)), "a clean launch left its slot not cleared"
+    _plant(pkg, dev, word, value)
+    got = run()
+    faults = N.attn_status(dev)
+    assert (faults > 0) == flagged, f"status {faults}, expected flagged={flagged}"
+    if whole:
+        for x, y in zip(got, ref):
+            assert torch.equal(x, y), "outputs of the dirty launch differ"
+    assert not any(_slot_words(pkg, dev)), "the slot was not reset"
+    again = run()
+    assert N.attn_status(dev) == 0
+    for x, y in zip(again, ref):
+        assert torch.equal(x, y), "the launch after the reset differs"
+    if flagged:  # the same through the Python check mode
+        prev = N.set_check_indices(True)
+        try:
+            _plant(pkg, dev, word, value)
+            with pytest.raises(N.LighthouseHipError, match="work-queue"):
+                run()
+        finally:
+            N.set_check_indices(prev)
+        assert not any(_slot_words(pkg, dev))
+        for x, y in zip(run(), ref):
+            assert torch.equal(x, y)
+
+
+def test_queue_two_graphs_on_two_streams(pkg, dev):
+    """Two graphs captured one after the other on torch's shared capture stream,
+    then replayed at the same time on two streams (and beside eager launches on
+    the default stream): each captured launch has counters of its own, so every
+    replay is bit-equal to the eager result and no slot is flagged."""
+    n, B, H = 30000, 1, 3
+    print(f"two graphs n={n} B={B} H={H}", flush=True)
+    N = pkg._native
+    xs = [_rand((B, n, H, 128), 120 + i, dev) for i in range(3)]
+    rows = N.Rows(*xs, (xs[0].stride(0), xs[0].stride(1), xs[0].stride(2)))
+    o, lse = N.attn_fwd(rows, None, B, H, n)
+    do = _rand((B, H, n, 128), 125, dev)
+    delta = (do.float() * o.float()).sum(-1)
+    ref = (o, lse) + N.attn_bwd(rows, None, B, H, n, do, lse, delta)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):  # warm-up off the capture
+        N.attn_fwd(rows, None, B, H, n)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graphs, outs = [], []
+    for _ in range(2):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs.append(N.attn_fwd(rows, None, B, H, n) + N.attn_bwd(rows, None, B, H, n, do, lse, delta))
+        graphs.append(g)
+    streams = [torch.cuda.Stream(dev), torch.cuda.Stream(dev)]
+    for r in range(3):
+        for out in outs:
+            for x in out:
+                x.zero_()
+        torch.cuda.synchronize(dev)
+        for g, s in zip(graphs, streams):
+            with torch.cuda.stream(s):
+                g.replay()
+        eager = N.attn_fwd(rows, None, B, H, n)
+        torch.cuda.synchronize(dev)
+        for i, out in enumerate(outs):
+            for name, x, y in zip(("o", "lse", "dq", "dk", "dv"), out, ref):
+                assert torch.equal(x, y), f"replay {r}, graph {i}: {name} differs from the eager result"
+        assert torch.equal(eager[0], ref[0])
+    assert N.attn_status(dev) == 0
