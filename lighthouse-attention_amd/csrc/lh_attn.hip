@@ -41,6 +41,7 @@
 #include <map>
 #include <mutex>
 #include <thread>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -726,6 +727,7 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArg
 // ===========================================================================
 // backward dQ (query-stationary)
 // ===========================================================================
+template <bool CTR>
 __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], float& rsum, const u32x4 (&qf)[8], const u32x4 (&df)[8],
                                         const bf16_t* Ks, const bf16_t* Vs, int k0, int my_q, int n, int lane,
                                         float sl2, float nlse, float dlt, bool mask) {
@@ -770,17 +772,19 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], float& rsum, const u
 #pragma unroll
     for (int v = 0; v < 16; ++v) s[v] = ex2(fmaf(s[v], sl2, nlse)) * dp[v];
     const u32x4 f0 = pack_frag(s, 0), f1 = pack_frag(s, 1);
-    {
-      // this lane's share of the row sum of the bf16 dS that the product below uses
+    if (CTR) {
+      // this lane's share of the row sum of the bf16 dS that the product below
+      // uses (two independent chains)
       const bf16x2 one = as_bf2(0x3f803f80u);
-      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.x), one, rsum, false);
-      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.y), one, rsum, false);
-      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.z), one, rsum, false);
-      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.w), one, rsum, false);
-      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.x), one, rsum, false);
-      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.y), one, rsum, false);
-      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.z), one, rsum, false);
-      rsum = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.w), one, rsum, false);
+      float r0 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.x), one, 0.f, false);
+      float r1 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.x), one, 0.f, false);
+      r0 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.y), one, r0, false);
+      r1 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.y), one, r1, false);
+      r0 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.z), one, r0, false);
+      r1 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.z), one, r1, false);
+      r0 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.w), one, r0, false);
+      r1 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.w), one, r1, false);
+      rsum += r0 + r1;
     }
     __builtin_amdgcn_s_setprio(1);
     {
@@ -815,7 +819,15 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], float& rsum, const u
 // end, which gives scale sum_t bf16(dS_it) (k_t - c): the rounding errors then
 // multiply k_t - c instead of k_t.  c is the fp32 mean of 64 key rows spread
 // evenly over the block's causal key range, read with plain loads beside the
-// first tile's direct loads (kc: 128 + 8 x 128 floats of LDS).
+// first tile's direct loads (kc: 128 + 8 x 129 floats of LDS).
+//
+// The row sum costs 16 VALU instructions per tile, which the VALU-bound loop
+// feels (+2.9% at cfg2), and it changes the result only where the keys share
+// a component: the errors it removes scale with |c|, those left with
+// |k_t - c|.  A block therefore applies it only when |c|^2 > E|k - c|^2 / 16
+// over the sample (|c| above a quarter of the keys' spread about it); N(0, 1)
+// keys (|c|^2 about 2 against 126) skip it and give the uncentred result.
+// Every wave forms the same sums in the same order, so the choice is uniform.
 __device__ __forceinline__ void dq_block(const AttnArgs& a, int bh, int qb, bf16_t* K0, bf16_t* K1, bf16_t* V0,
                                          bf16_t* V1, float* kc) {
   constexpr int BM = 32 * QW;
@@ -863,33 +875,57 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, int bh, int qb, bf16
     ks1 = ldg16((pooled ? m.kp : m.k) + o + 8 * ch);
   }
   wait_loads();
+  float* kcp = kc + 128;  // per wave: 128 dim sums, then the sum of squares
+  int ln = lane;  // opaque: its LDS addresses are not hoisted out of the block loop (they would spill)
+  asm volatile("" : "+v"(ln));
   {
     // sum the two rows, then over the four lanes of this wave that hold the
-    // same 8 dims, then over the waves in LDS
-    float c8[8];
+    // same 8 dims, then over the waves in LDS; beside it the sum of squares
+    float c8[8], k2 = 0.f;
     const uint32_t w0[4] = {ks0.x, ks0.y, ks0.z, ks0.w}, w1[4] = {ks1.x, ks1.y, ks1.z, ks1.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      c8[2 * e] = __uint_as_float(w0[e] << 16) + __uint_as_float(w1[e] << 16);
-      c8[2 * e + 1] = __uint_as_float(w0[e] & 0xffff0000u) + __uint_as_float(w1[e] & 0xffff0000u);
+      const float a0 = __uint_as_float(w0[e] << 16), a1 = __uint_as_float(w0[e] & 0xffff0000u);
+      const float b0 = __uint_as_float(w1[e] << 16), b1 = __uint_as_float(w1[e] & 0xffff0000u);
+      c8[2 * e] = a0 + b0;
+      c8[2 * e + 1] = a1 + b1;
+      k2 = fmaf(a0, a0, fmaf(a1, a1, fmaf(b0, b0, fmaf(b1, b1, k2))));
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       c8[e] += __shfl_xor(c8[e], 16);
       c8[e] += __shfl_xor(c8[e], 32);
     }
-    if (lane < 16) {
-      float4* dst = reinterpret_cast<float4*>(kc + 128 + wave * 128 + 8 * lane);
+#pragma unroll
+    for (int x = 1; x < 64; x <<= 1) k2 += __shfl_xor(k2, x);
+    if (ln < 16) {
+      float4* dst = reinterpret_cast<float4*>(kcp + wave * 132 + 8 * ln);
       dst[0] = float4{c8[0], c8[1], c8[2], c8[3]};
       dst[1] = float4{c8[4], c8[5], c8[6], c8[7]};
     }
+    if (ln == 0) kcp[wave * 132 + 128] = k2;
   }
   __syncthreads();
-  if (tid < 128) {
-    float c = 0.f;
+  bool ctr;
+  {
+    // every wave: lane l forms dims 2l, 2l+1 of the centre, the wave |c|^2,
+    // and all waves the same E|k|^2 (the same additions in the same order)
+    float ca = 0.f, cb = 0.f, kk = 0.f;
 #pragma unroll
-    for (int w = 0; w < QW; ++w) c += kc[128 + w * 128 + tid];
-    kc[tid] = c * (1.0f / 64.0f);  // read in the epilogue, past the step loop's barriers
+    for (int w = 0; w < QW; ++w) {
+      const float2 v = *reinterpret_cast<const float2*>(kcp + w * 132 + 2 * ln);
+      ca += v.x;
+      cb += v.y;
+      kk += kcp[w * 132 + 128];
+    }
+    ca *= 1.0f / 64.0f;
+    cb *= 1.0f / 64.0f;
+    float cc = fmaf(ca, ca, cb * cb);
+#pragma unroll
+    for (int x = 1; x < 64; x <<= 1) cc += __shfl_xor(cc, x);
+    // E|k - c|^2 = E|k|^2 - |c|^2 over the sample: centre when |c|^2 > that / 16
+    ctr = __builtin_amdgcn_readfirstlane((int)(17.0f * cc > kk * (1.0f / 64.0f)));
+    if (wave == 0) *reinterpret_cast<float2*>(kc + 2 * ln) = float2{ca, cb};  // read in the epilogue
   }
 
   floatx16 acc[4];
@@ -898,24 +934,32 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, int bh, int qb, bf16
   float rsum = 0.f;
   const int nfull = min((qw + 1) / BN, n / BN);
 
-  auto step = [&](int j, const bf16_t* Ks, const bf16_t* Vs, bf16_t* Kn, bf16_t* Vn) {
+  auto step = [&](auto C, int j, const bf16_t* Ks, const bf16_t* Vs, bf16_t* Kn, bf16_t* Vn) {
     const int k0 = j * BN;
     if (j + 1 < nt) issue_rows<QW>(Kn, m.k, m.kp, Vn, m.v, m.vp, m, rr, wave, lane);
     if (j + 2 < nt) load_rows<QW>(rr, m, k0 + 2 * BN, wave, lane);
     if (j < nt && k0 <= qw + 31)
-      dq_tile(acc, rsum, qf, df, Ks, Vs, k0, my_q, n, lane, a.sl2, nlse, dlt, j >= nfull);
+      dq_tile<decltype(C)::value>(acc, rsum, qf, df, Ks, Vs, k0, my_q, n, lane, a.sl2, nlse, dlt, j >= nfull);
     wait_loads();
     __syncthreads();
   };
-  for (int j = 0; j < nt; j += 2) {
-    step(j, K0, V0, K1, V1);
-    step(j + 1, K1, V1, K0, V0);
+  if (ctr) {
+    for (int j = 0; j < nt; j += 2) {
+      step(std::true_type{}, j, K0, V0, K1, V1);
+      step(std::true_type{}, j + 1, K1, V1, K0, V0);
+    }
+  } else {
+    for (int j = 0; j < nt; j += 2) {
+      step(std::false_type{}, j, K0, V0, K1, V1);
+      step(std::false_type{}, j + 1, K1, V1, K0, V0);
+    }
   }
 
   // the two lane halves hold the two halves of each row's keys
   rsum += __shfl_xor(rsum, 32);
   if (my_q >= n) return;
   // acc[d][4 g + e] is dim 32 d + 8 g + 4 hh + e
+  if (ctr)
 #pragma unroll
   for (int d = 0; d < 4; ++d)
 #pragma unroll
@@ -938,7 +982,7 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const Attn
   __shared__ __attribute__((aligned(1024))) bf16_t K1[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t V0[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t V1[TILE];
-  __shared__ __attribute__((aligned(16))) float KC[128 + QW * 128];  // key centre + per-wave partial sums
+  __shared__ __attribute__((aligned(16))) float KC[128 + QW * 132];  // key centre + per-wave partial sums
   __shared__ int wq_s[2];
   int bh, qb, bin = 0;
   bool have;

@@ -18,8 +18,9 @@ passes do.  With a large key component shared by the keys, sum_t dS[i, t] = 0
 cancels in fp32 but not after the rounding of each dS, and delta =
 rowsum(dO o O), formed from the bf16 O, errs along the same direction; the dQ
 kernel subtracts r_i c (r_i the row sum of the bf16 dS, c a mean of the block's
-keys), so its rounding errors multiply k_t - c instead of k_t.  That makes a
-component constant over the keys exact:
+keys) where the keys' mean is large against their spread (key_centres), so its
+rounding errors multiply k_t - c instead of k_t.  That makes a component
+constant over the keys exact:
   shared   - four channels of every key set to 32 (trained models' keys often
              have such channels): every output and gradient within the
              standard tolerance, at n = 1500 and through the whole layer at
@@ -66,15 +67,20 @@ BLOCK_Q = 256  # queries per block of the dQ kernel
 
 
 def key_centres(k):
-    """The dQ kernel's centre for each query ([B, H, n, D]): the fp32 mean of
+    """The dQ kernel's centre for each query ([B, H, n, D]): the fp32 mean c of
     the 64 keys (s kend) / 64, s < 64, of the query's block, kend the block's
-    causal key range (identity row map)."""
+    causal key range (identity row map), where the block centres, i.e. where
+    |c|^2 > E|k - c|^2 / 16 over those keys; zero elsewhere."""
     n = k.shape[2]
-    c = torch.empty_like(k)
+    c = torch.zeros_like(k)
     for q0 in range(0, n, BLOCK_Q):
         kend = min(q0 + BLOCK_Q, n)
         pos = (torch.arange(64) * kend) // 64
-        c[:, :, q0:kend] = k[:, :, pos].mean(2, keepdim=True)
+        ks = k[:, :, pos]
+        cm = ks.mean(2, keepdim=True)
+        cc = (cm * cm).sum(-1, keepdim=True)
+        kk = (ks * ks).sum(-1).mean(-1)[..., None, None]
+        c[:, :, q0:kend] = torch.where(17 * cc > kk, cm, torch.zeros_like(cm))
     return c
 
 
