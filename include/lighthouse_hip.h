@@ -40,7 +40,10 @@ extern "C" {
 #define LH_ERR_RUNTIME 5      /* a HIP runtime call (synchronize, copy, symbol lookup) failed */
 
 /* The ABI this header declares; lh_abi_version() of a matching library returns it. */
-#define LH_ABI_VERSION 6
+#define LH_ABI_VERSION 7
+
+#define LH_DTYPE_BF16 0       /* row element type: bfloat16 (the reference configs) */
+#define LH_DTYPE_F16 1        /* row element type: IEEE half */
 
 #define LH_TIE_REFERENCE 0    /* the reference network: strict compare-exchange only */
 #define LH_TIE_LOWER_INDEX 1  /* ties ordered by lower level-local index */
@@ -68,12 +71,17 @@ int lh_select_geometry(int S, int L, int p, int topk, int strict,
  * Norm scorer + Q/K/V pyramid, one streaming pass.
  * Replaces DialatedLighthouseNormScorer.forward (src/lighthouse_selection.py:589-616)
  * and the pyramid half of DilatedLighthouseScorer.forward (:655-689).
- *   xq, xk, xv      bf16 base rows, strides (sb, ss, sh) in elements, D contiguous
- *   pq, pk, pv      bf16 pooled rows written for levels 2..L, strides (pb, ps, ph)
+ *   xq, xk, xv      base rows of element type dtype (LH_DTYPE_BF16 / _F16),
+ *                   strides (sb, ss, sh) in elements, D contiguous
+ *   pq, pk, pv      pooled rows (dtype) written for levels 2..L, strides (pb, ps, ph)
  *   scores_qk/_kq   fp32 [B, H, S_tot] contiguous
- *   base_scores_given = 0: base-level scores are the bf16-rounded L2 norms of
- *     xq (qk) and xk (kq); = 1: base-level scores are already in scores_*
- *     (written by lh_dilated_scores) and only the max-pooled levels are made.
+ *   base_scores_given = 0: base-level scores are the L2 norms of xq (qk) and
+ *     xk (kq) rounded to dtype (torch's norm of such rows); = 1: base-level
+ *     scores are already in scores_* (written by lh_dilated_scores or
+ *     lh_gla_scores) and only the max-pooled levels are made.
+ * Every row-reading entry point of this library below takes the same dtype
+ * argument (its rows, outputs and rounding follow it; sums are fp32);
+ * the rotary and GLA entry points are bf16 only.
  */
 int lh_pyramid_fwd(const void *xq, const void *xk, const void *xv,
                    int64_t sb, int64_t ss, int64_t sh,
@@ -81,7 +89,7 @@ int lh_pyramid_fwd(const void *xq, const void *xk, const void *xv,
                    int64_t pb, int64_t ps, int64_t ph,
                    float *scores_qk, float *scores_kq,
                    int B, int S, int H, int D, int L, int p,
-                   int base_scores_given, void *stream);
+                   int base_scores_given, int dtype, void *stream);
 
 /*
  * Rotary embedding fused into the norm-scorer pyramid pass.
@@ -118,7 +126,8 @@ int lh_rope_pyramid_fwd(const void *xq, const void *xk, const void *xv,
  */
 int lh_dilated_scores(const void *xq, const void *xk, const void *xv,
                       float *scores_qk, float *scores_kq,
-                      int B, int S, int H, int D, int dilation, int S_tot, float scale, void *stream);
+                      int B, int S, int H, int D, int dilation, int S_tot, float scale, int dtype,
+                      void *stream);
 
 /*
  * GLA scorer base scores: the bf16-rounded L2 norms of the two simple gated
@@ -219,7 +228,7 @@ int lh_check_indices(const int32_t *indices, int B, int H, int n, int lo, int hi
 int lh_attn_fwd(const void *q, const void *k, const void *v, int64_t sb, int64_t ss, int64_t sh,
                 const void *qp, const void *kp, const void *vp, int64_t pb, int64_t ps, int64_t ph,
                 int split, const int32_t *indices, int B, int H, int n, int D, float scale,
-                void *out, float *lse, void *stream);
+                void *out, float *lse, int dtype, void *stream);
 
 /*
  * Causal attention backward over gathered rows (deterministic: dK/dV per key
@@ -235,7 +244,7 @@ int lh_attn_bwd(const void *q, const void *k, const void *v, int64_t sb, int64_t
                 const void *qp, const void *kp, const void *vp, int64_t pb, int64_t ps, int64_t ph,
                 int split, const int32_t *indices, int B, int H, int n, int D, float scale,
                 const void *dout, const float *lse, const float *delta,
-                void *dq, void *dk, void *dv, void *stream);
+                void *dq, void *dk, void *dv, int dtype, void *stream);
 
 /*
  * The two independent halves of lh_attn_bwd (same arguments), for callers that
@@ -246,12 +255,12 @@ int lh_attn_bwd_dkdv(const void *q, const void *k, const void *v, int64_t sb, in
                      const void *qp, const void *kp, const void *vp, int64_t pb, int64_t ps, int64_t ph,
                      int split, const int32_t *indices, int B, int H, int n, int D, float scale,
                      const void *dout, const float *lse, const float *delta,
-                     void *dk, void *dv, void *stream);
+                     void *dk, void *dv, int dtype, void *stream);
 int lh_attn_bwd_dq(const void *q, const void *k, const void *v, int64_t sb, int64_t ss, int64_t sh,
                    const void *qp, const void *kp, const void *vp, int64_t pb, int64_t ps, int64_t ph,
                    int split, const int32_t *indices, int B, int H, int n, int D, float scale,
                    const void *dout, const float *lse, const float *delta,
-                   void *dq, void *stream);
+                   void *dq, int dtype, void *stream);
 
 /*
  * Work-queue faults of the persistent attention launches (lh_attn_fwd,
@@ -289,7 +298,7 @@ int lh_attn_queue_slot(void *stream, void **slot);
  *   for [B, H, S_out, D] storage, (S_out*H*D, D, H*D) for [B, S_out, H, D] storage.
  */
 int lh_scatter_fwd(const void *attn, const int32_t *inverse, void *out, int64_t ob, int64_t oh, int64_t os,
-                   int B, int H, int S, int S_out, int n, int D, int L, int p, void *stream);
+                   int B, int H, int S, int S_out, int n, int D, int L, int p, int dtype, void *stream);
 
 /*
  * Adjoint of the fan-out: dattn[s] = sum of dout over the span of entry s,
@@ -300,7 +309,7 @@ int lh_scatter_fwd(const void *attn, const int32_t *inverse, void *out, int64_t 
  */
 int lh_scatter_bwd(const void *dout, int64_t db, int64_t dh, int64_t ds, const int32_t *indices, const void *o,
                    void *dattn, float *delta,
-                   int B, int H, int S, int S_out, int n, int D, int L, int p, void *stream);
+                   int B, int H, int S, int S_out, int n, int D, int L, int p, int dtype, void *stream);
 
 /*
  * Pyramid backward: dX[b,t,h] = g[inverse(t)] + sum_{l>=2} g[inverse(off_l + t/c_l)] / c_l
@@ -315,7 +324,7 @@ int lh_pyramid_bwd(const void *gq, const void *gk, const void *gv,
                    int64_t gb, int64_t gh, int64_t gs,
                    const int32_t *inverse,
                    void *dxq, void *dxk, void *dxv,
-                   int B, int S, int H, int D, int L, int p, void *stream);
+                   int B, int S, int H, int D, int L, int p, int dtype, void *stream);
 
 /*
  * Pyramid backward with the rotary embedding's backward fused in: as

@@ -37,26 +37,26 @@ _SIGS = {
     "lh_abi_version": (_I, []),
     "lh_select_geometry": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P]),
     "lh_pyramid_fwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _P, _P,
-                            _I, _I, _I, _I, _I, _I, _I, _P]),
-    "lh_dilated_scores": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P]),
+                            _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_dilated_scores": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P]),
     "lh_gla_scores": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _L, _P]),
     "lh_gla_workspace_bytes": (_L, [_I, _I, _I, _I, _I, _I]),
     "lh_select_topk": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_build_inverse": (_I, [_P, _I, _P, _I, _I, _I, _P]),
     "lh_check_indices": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "lh_attn_fwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _I, _P,
-                         _I, _I, _I, _I, _F, _P, _P, _P]),
+                         _I, _I, _I, _I, _F, _P, _P, _I, _P]),
     "lh_attn_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _I, _P,
-                         _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P]),
+                         _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _I, _P]),
     "lh_attn_bwd_dkdv": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _I, _P,
-                              _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P]),
+                              _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _I, _P]),
     "lh_attn_bwd_dq": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _I, _P,
-                            _I, _I, _I, _I, _F, _P, _P, _P, _P, _P]),
+                            _I, _I, _I, _I, _F, _P, _P, _P, _P, _I, _P]),
     "lh_attn_status": (_I, [_P]),
     "lh_attn_queue_slot": (_I, [_P, _P]),
-    "lh_scatter_fwd": (_I, [_P, _P, _P, _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
-    "lh_scatter_bwd": (_I, [_P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
-    "lh_pyramid_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_scatter_fwd": (_I, [_P, _P, _P, _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_scatter_bwd": (_I, [_P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "lh_pyramid_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_rope_pyramid_fwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L,
                                  _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "lh_pyramid_rope_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _P, _P, _L, _L, _L,
@@ -125,16 +125,30 @@ def _need_gpu(*ts):
             raise LighthouseHipError("lighthouse_hip kernels need GPU tensors (no CPU path)")
 
 
-def _need_rows(what, *ts):
-    """bf16 storage with a contiguous last (head) dimension: what every row-reading
-    kernel of the library assumes."""
+# Row element types of the native kernels (LH_DTYPE_* of the C ABI).
+ROW_DTYPES = {torch.bfloat16: 0, torch.float16: 1}
+
+
+def _need_rows(what, *ts, dtypes=ROW_DTYPES):
+    """16-bit float storage (bf16 or fp16, one type for all rows of a call) with a
+    contiguous last (head) dimension: what every row-reading kernel of the
+    library assumes.  Returns the dtype code (LH_DTYPE_BF16 / LH_DTYPE_F16)."""
+    code, first = None, None
     for t in ts:
         if t is None:
             continue
-        if t.dtype != torch.bfloat16:
-            raise TypeError(f"{what}: the native kernels read and write bfloat16 rows; got {t.dtype}")
+        if t.dtype not in dtypes:
+            names = " or ".join(str(d).replace("torch.", "") for d in dtypes)
+            raise TypeError(f"{what}: the native kernels read and write {names} rows; got {t.dtype}")
+        if first is not None and t.dtype != first:
+            raise TypeError(f"{what}: all rows of one call must share a dtype; got {first} and {t.dtype}")
+        first, code = t.dtype, dtypes[t.dtype]
         if t.dim() and t.stride(-1) != 1:
             raise ValueError(f"{what}: the head dimension must be contiguous (stride(-1) == 1)")
+    return 0 if code is None else code
+
+
+BF16_ONLY = {torch.bfloat16: 0}
 
 
 def _need_dtype(what, dtype, *ts):
@@ -200,25 +214,26 @@ def pyramid_lengths(S: int, L: int, p: int):
 # op wrappers (tensor in, tensor out; all on the current stream)
 # ---------------------------------------------------------------------------
 def pyramid_fwd(xq, xk, xv, L: int, p: int, scores=None, pooled_out=None):
-    """Norm scores + pooled Q/K/V.  ``xq/xk/xv`` bf16 [B, S, H, D] with D contiguous.
+    """Norm scores + pooled Q/K/V.  ``xq/xk/xv`` bf16 or fp16 [B, S, H, D] with D contiguous.
 
-    Returns ``(pq, pk, pv, scores_qk, scores_kq)`` with pooled rows bf16
-    [B, Sp, H, D] and scores fp32 [B, H, S_tot].  If ``scores`` is given
+    Returns ``(pq, pk, pv, scores_qk, scores_kq)`` with pooled rows of the input
+    dtype [B, Sp, H, D] and scores fp32 [B, H, S_tot].  If ``scores`` is given
     (dilated scorer), its base level is kept and only pooled.
     ``pooled_out`` may supply three pooled destinations (any strides, D contiguous).
     """
     _need_gpu(xq, xk, xv)
+    dt = _need_rows("pyramid_fwd", xq, xk, xv)
     B, S, H, D = xq.shape
     assert xk.shape == xq.shape and xv.shape == xq.shape
-    assert xq.dtype == torch.bfloat16 and xk.dtype == torch.bfloat16 and xv.dtype == torch.bfloat16
     assert xq.stride() == xk.stride() == xv.stride(), "q/k/v must share strides"
     lens, offs, S_tot = pyramid_lengths(S, L, p)
     Sp = S_tot - S
     dev = xq.device
     if pooled_out is None:
-        pq, pk, pv = (torch.empty(B, Sp, H, D, dtype=torch.bfloat16, device=dev) for _ in range(3))
+        pq, pk, pv = (torch.empty(B, Sp, H, D, dtype=xq.dtype, device=dev) for _ in range(3))
     else:
         pq, pk, pv = pooled_out
+        _need_rows("pyramid_fwd pooled_out", xq, pq, pk, pv)
     if scores is None:
         sqk = torch.empty(B, H, S_tot, dtype=torch.float32, device=dev)
         skq = torch.empty_like(sqk)
@@ -230,7 +245,7 @@ def pyramid_fwd(xq, xk, xv, L: int, p: int, scores=None, pooled_out=None):
     pb, ps, ph, _ = pq.stride()
     with torch.cuda.device(dev):
         rc = lib().lh_pyramid_fwd(_ptr(xq), _ptr(xk), _ptr(xv), sb, ss, sh, _ptr(pq), _ptr(pk), _ptr(pv),
-                                  pb, ps, ph, _ptr(sqk), _ptr(skq), B, S, H, D, L, p, given, _stream(dev))
+                                  pb, ps, ph, _ptr(sqk), _ptr(skq), B, S, H, D, L, p, given, dt, _stream(dev))
     _check(rc, "lh_pyramid_fwd")
     return pq, pk, pv, sqk, skq
 
@@ -251,7 +266,8 @@ def rope_pyramid_fwd(xqkv, freqs, H: int, L: int, p: int, D: int = D_SUPPORTED):
     ``xqkv``) share one set of strides; the rest as ``pyramid_fwd``."""
     _need_gpu(xqkv, freqs)
     B, S, W = xqkv.shape
-    assert W == 3 * H * D and xqkv.dtype == torch.bfloat16, "xqkv must hold [q | k | v] bf16 heads"
+    _need_rows("rope_pyramid_fwd", xqkv, dtypes=BF16_ONLY)
+    assert W == 3 * H * D, "xqkv must hold [q | k | v] heads"
     assert xqkv.stride(2) == 1 and xqkv.stride(0) == S * xqkv.stride(1), "rows of xqkv must be evenly strided"
     _check_freqs(freqs, S, D)
     lens, offs, S_tot = pyramid_lengths(S, L, p)
@@ -275,15 +291,16 @@ def rope_pyramid_fwd(xqkv, freqs, H: int, L: int, p: int, D: int = D_SUPPORTED):
 def dilated_scores(xq, xk, xv, dilation: int, S_tot: int, scale: float | None = None):
     """Base-level dilated scores into fresh fp32 [B, H, S_tot] buffers (pooled levels unset)."""
     _need_gpu(xq, xk, xv)
+    dt = _need_rows("dilated_scores", xq, xk, xv)
     B, S, H, D = xq.shape
     for t in (xq, xk, xv):
-        assert t.is_contiguous() and t.dtype == torch.bfloat16
+        assert t.is_contiguous()
     dev = xq.device
     sqk = torch.empty(B, H, S_tot, dtype=torch.float32, device=dev)
     skq = torch.empty_like(sqk)
     with torch.cuda.device(dev):
         rc = lib().lh_dilated_scores(_ptr(xq), _ptr(xk), _ptr(xv), _ptr(sqk), _ptr(skq), B, S, H, D, dilation,
-                                     S_tot, float(scale or 0.0), _stream(dev))
+                                     S_tot, float(scale or 0.0), dt, _stream(dev))
     _check(rc, "lh_dilated_scores")
     _check_queues(dev, "lh_dilated_scores")
     return sqk, skq
@@ -294,7 +311,7 @@ def gla_scores(xq, xk, xv, gk, dilation: int, S_tot: int, scale: float | None = 
     ``gk`` [B, S, H] log gates (any float dtype; taken in fp32, as fla does).
     ``segments``: sequence segments walked in parallel (0: chosen from the
     geometry so that every CU gets a workgroup; 1: one sequential walk)."""
-    _need_rows("gla_scores", xq, xk, xv)
+    _need_rows("gla_scores", xq, xk, xv, dtypes=BF16_ONLY)
     _need_gpu(xq, xk, xv, gk)
     B, S, H, D = xq.shape
     for t in (xq, xk, xv):
@@ -388,7 +405,8 @@ class Rows:
 
     def __init__(self, q, k, v, base_strides, qp=None, kp=None, vp=None, pool_strides=(0, 0, 0), split=None,
                  limit=None):
-        _need_rows("attention rows", q, k, v, qp, kp, vp)
+        self.dtype_code = _need_rows("attention rows", q, k, v, qp, kp, vp)
+        self.dtype = q.dtype
         self.q, self.k, self.v = q, k, v
         self.qp, self.kp, self.vp = qp, kp, vp
         self.bs = tuple(int(s) for s in base_strides)
@@ -409,6 +427,7 @@ class Rows:
 def _bwd_args_check(rows, indices, dout, lse, delta):
     _need_dtype("attention backward indices", torch.int32, indices)
     _need_rows("attention backward dout", dout)
+    _need_dtype("attention backward dout", rows.dtype, dout)
     _need_dtype("attention backward lse/delta", torch.float32, lse, delta)
     _need_gpu(rows.q, dout, lse, delta, indices)
     rows.check(indices)
@@ -417,17 +436,19 @@ def _bwd_args_check(rows, indices, dout, lse, delta):
 def attn_fwd(rows: Rows, indices, B: int, H: int, n: int, D: int = D_SUPPORTED, scale: float | None = None):
     """Causal attention over the rows named by ``indices`` [B, H, n] (None = identity).
 
-    Returns ``(O bf16 [B, H, n, D], lse fp32 [B, H, n])`` (lse in the exp2 domain)."""
+    Returns ``(O [B, H, n, D] of the rows' dtype, lse fp32 [B, H, n])`` (lse in the
+    exp2 domain)."""
     _need_dtype("attn_fwd indices", torch.int32, indices)
     _need_gpu(rows.q, indices)
     rows.check(indices)
     dev = rows.q.device
     scale = D ** -0.5 if scale is None else scale
     idx = indices.contiguous() if indices is not None else None
-    out = torch.empty(B, H, n, D, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(B, H, n, D, dtype=rows.dtype, device=dev)
     lse = torch.empty(B, H, n, dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
-        rc = lib().lh_attn_fwd(*rows.args(), _ptr(idx), B, H, n, D, scale, _ptr(out), _ptr(lse), _stream(dev))
+        rc = lib().lh_attn_fwd(*rows.args(), _ptr(idx), B, H, n, D, scale, _ptr(out), _ptr(lse), rows.dtype_code,
+                               _stream(dev))
     _check(rc, "lh_attn_fwd")
     _check_queues(dev, "lh_attn_fwd")
     return out, lse
@@ -435,15 +456,15 @@ def attn_fwd(rows: Rows, indices, B: int, H: int, n: int, D: int = D_SUPPORTED, 
 
 def attn_bwd_dkdv(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D: int = D_SUPPORTED,
                   scale: float | None = None):
-    """dK, dV of the gathered rows (key-stationary kernel): two bf16 [B, H, n, D]."""
+    """dK, dV of the gathered rows (key-stationary kernel): two [B, H, n, D] of the rows' dtype."""
     _bwd_args_check(rows, indices, dout, lse, delta)
     dev = rows.q.device
     scale = D ** -0.5 if scale is None else scale
     idx = indices.contiguous() if indices is not None else None
-    dk, dv = (torch.empty(B, H, n, D, dtype=torch.bfloat16, device=dev) for _ in range(2))
+    dk, dv = (torch.empty(B, H, n, D, dtype=rows.dtype, device=dev) for _ in range(2))
     with torch.cuda.device(dev):
         rc = lib().lh_attn_bwd_dkdv(*rows.args(), _ptr(idx), B, H, n, D, scale, _ptr(dout.contiguous()),
-                                    _ptr(lse), _ptr(delta), _ptr(dk), _ptr(dv), _stream(dev))
+                                    _ptr(lse), _ptr(delta), _ptr(dk), _ptr(dv), rows.dtype_code, _stream(dev))
     _check(rc, "lh_attn_bwd_dkdv")
     _check_queues(dev, "lh_attn_bwd_dkdv")
     return dk, dv
@@ -451,15 +472,15 @@ def attn_bwd_dkdv(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta,
 
 def attn_bwd_dq(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D: int = D_SUPPORTED,
                 scale: float | None = None):
-    """dQ of the gathered rows (query-stationary kernel): bf16 [B, H, n, D]."""
+    """dQ of the gathered rows (query-stationary kernel): [B, H, n, D] of the rows' dtype."""
     _bwd_args_check(rows, indices, dout, lse, delta)
     dev = rows.q.device
     scale = D ** -0.5 if scale is None else scale
     idx = indices.contiguous() if indices is not None else None
-    dq = torch.empty(B, H, n, D, dtype=torch.bfloat16, device=dev)
+    dq = torch.empty(B, H, n, D, dtype=rows.dtype, device=dev)
     with torch.cuda.device(dev):
         rc = lib().lh_attn_bwd_dq(*rows.args(), _ptr(idx), B, H, n, D, scale, _ptr(dout.contiguous()),
-                                  _ptr(lse), _ptr(delta), _ptr(dq), _stream(dev))
+                                  _ptr(lse), _ptr(delta), _ptr(dq), rows.dtype_code, _stream(dev))
     _check(rc, "lh_attn_bwd_dq")
     _check_queues(dev, "lh_attn_bwd_dq")
     return dq
@@ -467,16 +488,16 @@ def attn_bwd_dq(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D
 
 def attn_bwd(rows: Rows, indices, B: int, H: int, n: int, dout, lse, delta, D: int = D_SUPPORTED,
              scale: float | None = None):
-    """Gradients w.r.t. the gathered q, k, v rows: three bf16 [B, H, n, D]."""
+    """Gradients w.r.t. the gathered q, k, v rows: three [B, H, n, D] of the rows' dtype."""
     _bwd_args_check(rows, indices, dout, lse, delta)
     dev = rows.q.device
     scale = D ** -0.5 if scale is None else scale
     idx = indices.contiguous() if indices is not None else None
     dout = dout.contiguous()
-    dq, dk, dv = (torch.empty(B, H, n, D, dtype=torch.bfloat16, device=dev) for _ in range(3))
+    dq, dk, dv = (torch.empty(B, H, n, D, dtype=rows.dtype, device=dev) for _ in range(3))
     with torch.cuda.device(dev):
         rc = lib().lh_attn_bwd(*rows.args(), _ptr(idx), B, H, n, D, scale, _ptr(dout), _ptr(lse), _ptr(delta),
-                               _ptr(dq), _ptr(dk), _ptr(dv), _stream(dev))
+                               _ptr(dq), _ptr(dk), _ptr(dv), rows.dtype_code, _stream(dev))
     _check(rc, "lh_attn_bwd")
     _check_queues(dev, "lh_attn_bwd")
     return dq, dk, dv
@@ -487,7 +508,7 @@ def scatter_fwd(attn, inverse, S: int, S_out: int, L: int, p: int, seq_major: bo
 
     ``seq_major`` stores the result as ``[B, S_out, H, D]`` and returns its
     ``[B, H, S_out, D]`` view (transposing it back is then free)."""
-    _need_rows("scatter_fwd attn", attn)
+    dt = _need_rows("scatter_fwd attn", attn)
     _need_dtype("scatter_fwd inverse", torch.int32, inverse)
     _need_gpu(attn, inverse)
     attn = attn.contiguous()
@@ -501,15 +522,15 @@ def scatter_fwd(attn, inverse, S: int, S_out: int, L: int, p: int, seq_major: bo
     ob, oh, os_, od = out.stride()
     with torch.cuda.device(attn.device):
         rc = lib().lh_scatter_fwd(_ptr(attn), _ptr(inverse), _ptr(out), ob, oh, os_, B, H, S, S_out, n, D, L, p,
-                                  _stream(attn.device))
+                                  dt, _stream(attn.device))
     _check(rc, "lh_scatter_fwd")
     return out
 
 
 def scatter_bwd(dout, indices, o, S: int, L: int, p: int):
-    """``(dattn bf16 [B, H, n, D], delta fp32 [B, H, n] or None)``; ``dout`` may have
-    any (batch, head, seq) strides with D contiguous."""
-    _need_rows("scatter_bwd", dout, o)
+    """``(dattn [B, H, n, D] of dout's dtype, delta fp32 [B, H, n] or None)``; ``dout``
+    may have any (batch, head, seq) strides with D contiguous."""
+    dt = _need_rows("scatter_bwd", dout, o)
     _need_dtype("scatter_bwd indices", torch.int32, indices)
     _need_gpu(dout, indices, o)
     if _check_indices:
@@ -524,29 +545,29 @@ def scatter_bwd(dout, indices, o, S: int, L: int, p: int):
     db, dh, ds, _ = dout.stride()
     with torch.cuda.device(dout.device):
         rc = lib().lh_scatter_bwd(_ptr(dout), db, dh, ds, _ptr(indices.contiguous()), _ptr(oc), _ptr(dattn),
-                                  _ptr(delta), B, H, S, S_out, n, D, L, p, _stream(dout.device))
+                                  _ptr(delta), B, H, S, S_out, n, D, L, p, dt, _stream(dout.device))
     _check(rc, "lh_scatter_bwd")
     return dattn, delta
 
 
 def pyramid_bwd(gq, gk, gv, inverse, B: int, S: int, H: int, L: int, p: int, D: int = D_SUPPORTED):
-    """Base-row gradients bf16 [B, S, H, D] from selected-space (or pyramid-row) grads
-    ``g*`` indexed [b, h, s, :] with any strides (D contiguous)."""
-    _need_rows("pyramid_bwd grads", gq, gk, gv)
+    """Base-row gradients [B, S, H, D] (the grads' dtype) from selected-space (or
+    pyramid-row) grads ``g*`` indexed [b, h, s, :] with any strides (D contiguous)."""
+    dt = _need_rows("pyramid_bwd grads", gq, gk, gv)
     _need_dtype("pyramid_bwd inverse", torch.int32, inverse)
     ref = next(g for g in (gq, gk, gv) if g is not None)
     _need_gpu(ref, inverse)
     if _check_indices and inverse is not None:
         check_indices(inverse, -1, ref.shape[2], unique=False, what="pyramid_bwd inverse map")
     dev = ref.device
-    outs = [torch.empty(B, S, H, D, dtype=torch.bfloat16, device=dev) if g is not None else None
+    outs = [torch.empty(B, S, H, D, dtype=ref.dtype, device=dev) if g is not None else None
             for g in (gq, gk, gv)]
     gb, gh, gs, _ = ref.stride()
     for g in (gq, gk, gv):
         assert g is None or tuple(g.stride()) == (gb, gh, gs, 1), "selected grads must share strides"
     with torch.cuda.device(dev):
         rc = lib().lh_pyramid_bwd(_ptr(gq), _ptr(gk), _ptr(gv), gb, gh, gs, _ptr(inverse),
-                                  _ptr(outs[0]), _ptr(outs[1]), _ptr(outs[2]), B, S, H, D, L, p, _stream(dev))
+                                  _ptr(outs[0]), _ptr(outs[1]), _ptr(outs[2]), B, S, H, D, L, p, dt, _stream(dev))
     _check(rc, "lh_pyramid_bwd")
     return tuple(outs)
 
@@ -555,7 +576,7 @@ def pyramid_rope_bwd(gq, gk, gv, inverse, freqs, B: int, S: int, H: int, L: int,
     """``pyramid_bwd`` with the rotary embedding's backward fused in: returns the
     gradient of the fused projection output, bf16 [B, S, 3*H*D] ([dq | dk | dv],
     dq and dk rotated back by -theta)."""
-    _need_rows("pyramid_rope_bwd grads", gq, gk, gv)
+    _need_rows("pyramid_rope_bwd grads", gq, gk, gv, dtypes=BF16_ONLY)
     _need_gpu(gq, gk, gv)
     _check_freqs(freqs, S, D)
     gb, gh, gs, _ = gq.stride()
@@ -581,6 +602,7 @@ def rope_qkv_fwd(x, freqs, Hq: int, Hkv: int, D: int = D_SUPPORTED):
     exceed the width; D contiguous) into q, k, v [B, S, H, D] contiguous, with q and
     k rotated by ``freqs`` (fp32 [>=S, D/2, 2] = cos, sin)."""
     _need_gpu(x, freqs)
+    _need_dtype("rope_qkv_fwd (bf16 only)", torch.bfloat16, x)
     B, S, W = x.shape
     assert x.stride(2) == 1 and x.stride(0) == S * x.stride(1), "rows of x must be evenly strided"
     assert W == (Hq + 2 * Hkv) * D, "x must hold [q | k | v] heads"
@@ -601,6 +623,7 @@ def rope_qkv_bwd(dq, dk, dv, freqs, Hq: int, Hkv: int, D: int = D_SUPPORTED):
     """Adjoint of ``rope_qkv_fwd``: grads of q, k, v ([B, S, H, D], any strides with D
     contiguous) -> grad of the fused projection output [B, S, (Hq+2Hkv)*D]."""
     _need_gpu(dq, dk, dv, freqs)
+    _need_dtype("rope_qkv_bwd (bf16 only)", torch.bfloat16, dq, dk, dv)
     B, S = dq.shape[:2]
     assert tuple(dq.shape) == (B, S, Hq, D) and tuple(dk.shape) == (B, S, Hkv, D) == tuple(dv.shape)
     assert freqs.dtype == torch.float32 and freqs.is_contiguous() and tuple(freqs.shape[1:]) == (D // 2, 2) \
@@ -620,6 +643,7 @@ def rope_qkv_bwd(dq, dk, dv, freqs, Hq: int, Hkv: int, D: int = D_SUPPORTED):
 def rmsnorm_fwd(x, w, eps: float):
     """``y = (x * rsqrt(mean(x^2) + eps)) * w`` over the last dim; returns (y, rstd fp32)."""
     _need_gpu(x, w)
+    _need_dtype("rmsnorm_fwd (bf16 only)", torch.bfloat16, x, w)
     x = x.contiguous()
     dim = x.shape[-1]
     assert w.shape == (dim,) and w.is_contiguous(), "weight must be [dim]"
@@ -635,6 +659,7 @@ def rmsnorm_fwd(x, w, eps: float):
 def add_rmsnorm_fwd(x, r, w, eps: float):
     """``h = x + r`` (bf16) and ``y = RMSNorm(h)``; returns ``(h, y, rstd)``."""
     _need_gpu(x, r, w)
+    _need_dtype("add_rmsnorm_fwd (bf16 only)", torch.bfloat16, x, r, w)
     x, r = x.contiguous(), r.contiguous()
     dim = x.shape[-1]
     rows = x.numel() // dim
@@ -656,6 +681,7 @@ def rmsnorm_bwd(dy, x, w, rstd, dres=None):
     """Grads of RMSNorm: ``(dx bf16 like x, dw bf16 like w)``; ``dres`` (optional) is
     added to dx (a residual branch's gradient)."""
     _need_gpu(dy, x, w, rstd)
+    _need_dtype("rmsnorm_bwd (bf16 only)", torch.bfloat16, dy, x, w)
     dy, x, rstd = dy.contiguous(), x.contiguous(), rstd.contiguous()
     if dres is not None:
         dres = dres.contiguous()
@@ -675,6 +701,7 @@ def rmsnorm_bwd(dy, x, w, rstd, dres=None):
 def swiglu_fwd(h):
     """``h`` [..., 2F] = [h1 | h3] -> ``silu(h1) * h3`` [..., F] (torch's roundings)."""
     _need_gpu(h)
+    _need_dtype("swiglu_fwd (bf16 only)", torch.bfloat16, h)
     h = h.contiguous()
     F2 = h.shape[-1]
     rows = h.numel() // F2
@@ -687,6 +714,7 @@ def swiglu_fwd(h):
 
 def swiglu_bwd(da, h):
     _need_gpu(da, h)
+    _need_dtype("swiglu_bwd (bf16 only)", torch.bfloat16, da, h)
     da, h = da.contiguous(), h.contiguous()
     F2 = h.shape[-1]
     rows = h.numel() // F2

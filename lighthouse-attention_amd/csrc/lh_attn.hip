@@ -59,6 +59,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((__vector_size__(8 * sizeof(_Float16))));
 
 struct Rows {
   const bf16_t *q, *k, *v, *qp, *kp, *vp;
@@ -112,22 +113,45 @@ __device__ __forceinline__ uint32_t row_off(const BhRows& m, int s, bool& pooled
   return pooled ? (uint32_t)(r - m.split) * (uint32_t)m.ps : (uint32_t)r * (uint32_t)m.ss;
 }
 
+// The attention kernels run on bf16 or fp16 rows (element type T, BF16 or F16):
+// the matrix-core product, the rounding of P / dS / outputs and the row sums of
+// the rounded values follow T; everything else is type-free 16-bit data.
+template <typename T>
 __device__ __forceinline__ floatx16 mfma(const u32x4 a, const u32x4 b, const floatx16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
-                                                 0, 0);
+  if constexpr (std::is_same_v<T, F16>)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
 }
 
+template <typename T>
 __device__ __forceinline__ uint32_t cvt2(float lo, float hi) {
-  f32x2 v = {lo, hi};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  return T::pack2(lo, hi);
 }
 
-// two packed bf16 as the vector type of the dot builtins (a memcpy: this
-// compiler mis-lowers __builtin_bit_cast of a single vector element)
+// two packed 16-bit values as the vector type of the dot builtins (a memcpy:
+// this compiler mis-lowers __builtin_bit_cast of a single vector element)
 __device__ __forceinline__ bf16x2 as_bf2(uint32_t u) {
   bf16x2 r;
   __builtin_memcpy(&r, &u, 4);
   return r;
+}
+__device__ __forceinline__ lh_f16x2 as_h2(uint32_t u) {
+  lh_f16x2 r;
+  __builtin_memcpy(&r, &u, 4);
+  return r;
+}
+
+// acc + the two values packed in u (exact products with 1, fp32 sum): row sums
+// of rounded operands, two terms per v_dot2
+template <typename T>
+__device__ __forceinline__ float dot2one(uint32_t u, float acc) {
+  if constexpr (std::is_same_v<T, F16>)
+    return __builtin_amdgcn_fdot2(as_h2(u), as_h2(0x3c003c00u), acc, false);
+  else
+    return __builtin_amdgcn_fdot2_f32_bf16(as_bf2(u), as_bf2(0x3f803f80u), acc, false);
 }
 
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -489,22 +513,24 @@ __device__ __forceinline__ u32x4 lds_tr(const bf16_t* tile, const LaneLds& ll, i
 }
 
 // 8 fp32 accumulator values v = 8*c2 .. 8*c2+7 -> bf16 B operand
+template <typename T>
 __device__ __forceinline__ u32x4 pack_frag(const floatx16& s, int c2) {
   const int v = 8 * c2;
-  return u32x4{cvt2(s[v + 0], s[v + 1]), cvt2(s[v + 2], s[v + 3]), cvt2(s[v + 4], s[v + 5]), cvt2(s[v + 6], s[v + 7])};
+  return u32x4{cvt2<T>(s[v + 0], s[v + 1]), cvt2<T>(s[v + 2], s[v + 3]), cvt2<T>(s[v + 4], s[v + 5]), cvt2<T>(s[v + 6], s[v + 7])};
 }
 
 // key index held in accumulator slot v of a 32-key block
 __device__ __forceinline__ int slot_key(int v, int hh) { return 8 * (v >> 2) + 4 * hh + (v & 3); }
 
-__device__ __forceinline__ void store_rows_bf16(bf16_t* row, const floatx16 (&acc)[4], float sc, int hh) {
+template <typename T>
+__device__ __forceinline__ void store_rows(bf16_t* row, const floatx16 (&acc)[4], float sc, int hh) {
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       u32x2 w;
-      w.x = cvt2(acc[d][4 * g + 0] * sc, acc[d][4 * g + 1] * sc);
-      w.y = cvt2(acc[d][4 * g + 2] * sc, acc[d][4 * g + 3] * sc);
+      w.x = cvt2<T>(acc[d][4 * g + 0] * sc, acc[d][4 * g + 1] * sc);
+      w.y = cvt2<T>(acc[d][4 * g + 2] * sc, acc[d][4 * g + 3] * sc);
       *reinterpret_cast<u32x2*>(row + d * 32 + 8 * g + 4 * hh) = w;
     }
   }
@@ -522,6 +548,7 @@ struct FwdState {
   float l;  // this lane's half of the row sum
 };
 
+template <typename T>
 __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], const bf16_t* Ks, const bf16_t* Vs,
                                          int k0, int my_q, int n, int lane, float sl2, bool mask) {
   const int hh = lane >> 5;
@@ -533,10 +560,10 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
     u32x4 kf[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) kf[i] = lds_row(Ks, ll, i & 1, i >> 1);
-    s[0] = mfma(kf[0], qf[0], floatx16{});
-    s[1] = mfma(kf[1], qf[0], floatx16{});
+    s[0] = mfma<T>(kf[0], qf[0], floatx16{});
+    s[1] = mfma<T>(kf[1], qf[0], floatx16{});
 #pragma unroll
-    for (int i = 2; i < 16; ++i) s[i & 1] = mfma(kf[i], qf[i >> 1], s[i & 1]);
+    for (int i = 2; i < 16; ++i) s[i & 1] = mfma<T>(kf[i], qf[i >> 1], s[i & 1]);
     SCHED_GROUP(SG_DSR, FWD_AHEAD);
 #pragma unroll
     for (int i = 0; i < 16 - FWD_AHEAD; ++i) {
@@ -580,23 +607,22 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
   u32x4 pf[2][2];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
-    pf[kb][0] = pack_frag(s[kb], 0);
-    pf[kb][1] = pack_frag(s[kb], 1);
+    pf[kb][0] = pack_frag<T>(s[kb], 0);
+    pf[kb][1] = pack_frag<T>(s[kb], 1);
   }
   // Row sum of the bf16 P that the P V product uses, two terms per v_dot2
   // (16 instructions instead of 32 adds); the weights of O then sum to 1
   // exactly, up to the fp32 accumulation.
   {
-    const bf16x2 one = as_bf2(0x3f803f80u);
     float ls = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        ls = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(pf[kb][h].x), one, ls, false);
-        ls = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(pf[kb][h].y), one, ls, false);
-        ls = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(pf[kb][h].z), one, ls, false);
-        ls = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(pf[kb][h].w), one, ls, false);
+        ls = dot2one<T>(pf[kb][h].x, ls);
+        ls = dot2one<T>(pf[kb][h].y, ls);
+        ls = dot2one<T>(pf[kb][h].z, ls);
+        ls = dot2one<T>(pf[kb][h].w, ls);
       }
     st.l += ls;
   }
@@ -608,7 +634,7 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
 #pragma unroll
     for (int i = 0; i < 16; ++i) vf[i] = lds_tr(Vs, ll, (i >> 3) * 32 + 16 * ((i >> 2) & 1), i & 3);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) st.o[i & 3] = mfma(vf[i], pf[i >> 3][(i >> 2) & 1], st.o[i & 3]);
+    for (int i = 0; i < 16; ++i) st.o[i & 3] = mfma<T>(vf[i], pf[i >> 3][(i >> 2) & 1], st.o[i & 3]);
     SCHED_GROUP(SG_DSR, 2 * FWD_AHEAD);
 #pragma unroll
     for (int i = 0; i < 16 - FWD_AHEAD; ++i) {
@@ -620,7 +646,7 @@ __device__ __forceinline__ void fwd_tile(FwdState& st, const u32x4 (&qf)[8], con
 }
 
 // One query block qb of (b, h) bh.
-template <int EPI>  // 0: O + LSE;  1: bf16-rounded row norms of O into `scores`
+template <typename T, int EPI>  // 0: O + LSE;  1: rounded row norms of O into `scores`
 __device__ __forceinline__ void fwd_block(const AttnArgs& a, int bh, int qb, bf16_t* K0, bf16_t* K1, bf16_t* V0,
                                           bf16_t* V1) {
   constexpr int BM = 32 * QW;
@@ -660,7 +686,7 @@ __device__ __forceinline__ void fwd_block(const AttnArgs& a, int bh, int qb, bf1
     const int k0 = j * BN;
     if (j + 1 < nt) issue_rows<QW>(Kn, m.k, m.kp, Vn, m.v, m.vp, m, rr, wave, lane);
     if (j + 2 < nt) load_rows<QW>(rr, m, k0 + 2 * BN, wave, lane);
-    if (j < nt && k0 <= qw + 31) fwd_tile(st, qf, Ks, Vs, k0, my_q, n, lane, a.sl2, j >= nfull);
+    if (j < nt && k0 <= qw + 31) fwd_tile<T>(st, qf, Ks, Vs, k0, my_q, n, lane, a.sl2, j >= nfull);
     wait_loads();
     __syncthreads();
   };
@@ -673,7 +699,7 @@ __device__ __forceinline__ void fwd_block(const AttnArgs& a, int bh, int qb, bf1
   const float l = st.l + __shfl_xor(st.l, 32);
   const float inv_l = l > 0.f ? 1.0f / l : 0.f;
   if (EPI == 0) {
-    store_rows_bf16(a.out + ((int64_t)bh * n + my_q) * LH_D, st.o, inv_l, hh);
+    store_rows<T>(a.out + ((int64_t)bh * n + my_q) * LH_D, st.o, inv_l, hh);
     if (hh == 0) a.lse[(int64_t)bh * n + my_q] = l > 0.f ? st.m * a.sl2 + __log2f(l) : -INFINITY;
   } else {
     float ss = 0.f;
@@ -681,8 +707,8 @@ __device__ __forceinline__ void fwd_block(const AttnArgs& a, int bh, int qb, bf1
     for (int d = 0; d < 4; ++d) {
 #pragma unroll
       for (int v = 0; v < 16; v += 2) {
-        const uint32_t w = cvt2(st.o[d][v] * inv_l, st.o[d][v + 1] * inv_l);
-        const float x0 = __uint_as_float(w << 16), x1 = __uint_as_float(w & 0xffff0000u);
+        const uint32_t w = cvt2<T>(st.o[d][v] * inv_l, st.o[d][v + 1] * inv_l);
+        const float x0 = T::lo(w), x1 = T::hi(w);
         ss = fmaf(x0, x0, ss);
         ss = fmaf(x1, x1, ss);
       }
@@ -693,12 +719,12 @@ __device__ __forceinline__ void fwd_block(const AttnArgs& a, int bh, int qb, bf1
       const int b = bh / a.H;
       const int t = my_q * a.dil + vh / a.Ho;
       const int ho = vh % a.Ho;
-      a.scores[((int64_t)b * a.Ho + ho) * a.S_tot + t] = __uint_as_float(cvt2(sqrtf(ss), 0.f) << 16);
+      a.scores[((int64_t)b * a.Ho + ho) * a.S_tot + t] = round_to<T>(sqrtf(ss));
     }
   }
 }
 
-template <int EPI>
+template <typename T, int EPI>
 __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArgs a, const QPlan p, const WorkQ q) {
   __shared__ __attribute__((aligned(1024))) bf16_t K0[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t K1[TILE];
@@ -715,7 +741,7 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArg
     if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, true, -1, 0, bh, qb, wq_s);
   }
   for (int k = 1; have; ++k) {
-    fwd_block<EPI>(a, bh, qb, K0, K1, V0, V1);
+    fwd_block<T, EPI>(a, bh, qb, K0, K1, V0, V1);
     // the next block starts after this one's last tile reads
     if (p.bph)
       have = plan_next(p, bin, k, qb);
@@ -727,7 +753,7 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_fwd_kernel(const AttnArg
 // ===========================================================================
 // backward dQ (query-stationary)
 // ===========================================================================
-template <bool CTR>
+template <typename T, bool CTR>
 __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], float& rsum, const u32x4 (&qf)[8], const u32x4 (&df)[8],
                                         const bf16_t* Ks, const bf16_t* Vs, int k0, int my_q, int n, int lane,
                                         float sl2, float nlse, float dlt, bool mask) {
@@ -746,12 +772,12 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], float& rsum, const u
       floatx16 dinit;
 #pragma unroll
       for (int v = 0; v < 16; ++v) dinit[v] = -dlt;  // the accumulator ends as dP - delta
-      s = mfma(f[0], qf[0], floatx16{});
-      dp = mfma(f[1], df[0], dinit);
+      s = mfma<T>(f[0], qf[0], floatx16{});
+      dp = mfma<T>(f[1], df[0], dinit);
 #pragma unroll
       for (int i = 2; i < 16; i += 2) {
-        s = mfma(f[i], qf[i >> 1], s);
-        dp = mfma(f[i + 1], df[i >> 1], dp);
+        s = mfma<T>(f[i], qf[i >> 1], s);
+        dp = mfma<T>(f[i + 1], df[i >> 1], dp);
       }
       SCHED_GROUP(SG_DSR, DQ_AHEAD);
 #pragma unroll
@@ -771,19 +797,18 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], float& rsum, const u
     }
 #pragma unroll
     for (int v = 0; v < 16; ++v) s[v] = ex2(fmaf(s[v], sl2, nlse)) * dp[v];
-    const u32x4 f0 = pack_frag(s, 0), f1 = pack_frag(s, 1);
+    const u32x4 f0 = pack_frag<T>(s, 0), f1 = pack_frag<T>(s, 1);
     if (CTR) {
       // this lane's share of the row sum of the bf16 dS that the product below
       // uses (two independent chains)
-      const bf16x2 one = as_bf2(0x3f803f80u);
-      float r0 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.x), one, 0.f, false);
-      float r1 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.x), one, 0.f, false);
-      r0 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.y), one, r0, false);
-      r1 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.y), one, r1, false);
-      r0 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.z), one, r0, false);
-      r1 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.z), one, r1, false);
-      r0 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f0.w), one, r0, false);
-      r1 = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(f1.w), one, r1, false);
+      float r0 = dot2one<T>(f0.x, 0.f);
+      float r1 = dot2one<T>(f1.x, 0.f);
+      r0 = dot2one<T>(f0.y, r0);
+      r1 = dot2one<T>(f1.y, r1);
+      r0 = dot2one<T>(f0.z, r0);
+      r1 = dot2one<T>(f1.z, r1);
+      r0 = dot2one<T>(f0.w, r0);
+      r1 = dot2one<T>(f1.w, r1);
       rsum += r0 + r1;
     }
     __builtin_amdgcn_s_setprio(1);
@@ -793,7 +818,7 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], float& rsum, const u
 #pragma unroll
       for (int i = 0; i < 8; ++i) g[i] = lds_tr(Ks, ll, kb * 32 + 16 * (i >> 2), i & 3);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i & 3] = mfma(g[i], (i >> 2) ? f1 : f0, acc[i & 3]);
+      for (int i = 0; i < 8; ++i) acc[i & 3] = mfma<T>(g[i], (i >> 2) ? f1 : f0, acc[i & 3]);
       SCHED_GROUP(SG_DSR, 2 * DQ_AHEAD2);
 #pragma unroll
       for (int i = 0; i < 8 - DQ_AHEAD2; ++i) {
@@ -828,6 +853,7 @@ __device__ __forceinline__ void dq_tile(floatx16 (&acc)[4], float& rsum, const u
 // over the sample (|c| above a quarter of the keys' spread about it); N(0, 1)
 // keys (|c|^2 about 2 against 126) skip it and give the uncentred result.
 // Every wave forms the same sums in the same order, so the choice is uniform.
+template <typename T>
 __device__ __forceinline__ void dq_block(const AttnArgs& a, int bh, int qb, bf16_t* K0, bf16_t* K1, bf16_t* V0,
                                          bf16_t* V1, float* kc) {
   constexpr int BM = 32 * QW;
@@ -885,8 +911,8 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, int bh, int qb, bf16
     const uint32_t w0[4] = {ks0.x, ks0.y, ks0.z, ks0.w}, w1[4] = {ks1.x, ks1.y, ks1.z, ks1.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float a0 = __uint_as_float(w0[e] << 16), a1 = __uint_as_float(w0[e] & 0xffff0000u);
-      const float b0 = __uint_as_float(w1[e] << 16), b1 = __uint_as_float(w1[e] & 0xffff0000u);
+      const float a0 = T::lo(w0[e]), a1 = T::hi(w0[e]);
+      const float b0 = T::lo(w1[e]), b1 = T::hi(w1[e]);
       c8[2 * e] = a0 + b0;
       c8[2 * e + 1] = a1 + b1;
       k2 = fmaf(a0, a0, fmaf(a1, a1, fmaf(b0, b0, fmaf(b1, b1, k2))));
@@ -939,7 +965,7 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, int bh, int qb, bf16
     if (j + 1 < nt) issue_rows<QW>(Kn, m.k, m.kp, Vn, m.v, m.vp, m, rr, wave, lane);
     if (j + 2 < nt) load_rows<QW>(rr, m, k0 + 2 * BN, wave, lane);
     if (j < nt && k0 <= qw + 31)
-      dq_tile<decltype(C)::value>(acc, rsum, qf, df, Ks, Vs, k0, my_q, n, lane, a.sl2, nlse, dlt, j >= nfull);
+      dq_tile<T, decltype(C)::value>(acc, rsum, qf, df, Ks, Vs, k0, my_q, n, lane, a.sl2, nlse, dlt, j >= nfull);
     wait_loads();
     __syncthreads();
   };
@@ -973,10 +999,11 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, int bh, int qb, bf16
   {
     int row = my_q, half = hh;
     asm volatile("" : "+v"(row), "+v"(half));
-    store_rows_bf16(a.dq + ((int64_t)bh * n + row) * LH_D, acc, a.scale, half);
+    store_rows<T>(a.dq + ((int64_t)bh * n + row) * LH_D, acc, a.scale, half);
   }
 }
 
+template <typename T>
 __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const AttnArgs a, const QPlan p, const WorkQ q) {
   __shared__ __attribute__((aligned(1024))) bf16_t K0[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t K1[TILE];
@@ -994,7 +1021,7 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void attn_bwd_dq_kernel(const Attn
     if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, true, -1, 0, bh, qb, wq_s);
   }
   for (int k = 1; have; ++k) {
-    dq_block(a, bh, qb, K0, K1, V0, V1, KC);
+    dq_block<T>(a, bh, qb, K0, K1, V0, V1, KC);
     // the next block starts after this one's last tile reads
     if (p.bph)
       have = plan_next(p, bin, k, qb);
@@ -1119,6 +1146,7 @@ __device__ __forceinline__ void s_start(floatx16& a, const float* lse, float nis
 
 // MFMA phase of a P wave: dV += dO^T P of the previous tile (Dp, pp), then
 // S of the current tile (Qc).  Operands are read a group ahead of their MFMAs.
+template <typename T>
 __device__ __forceinline__ void pw_mma(floatx16 (&s)[2], floatx16 (&dva)[4], const u32x4 (&kf)[8],
                                        const u32x4 (&pp)[2][2], const bf16_t* Qc, const bf16_t* Dp,
                                        const LaneLds& ll, const float* lse, float nisl2) {
@@ -1133,25 +1161,26 @@ __device__ __forceinline__ void pw_mma(floatx16 (&s)[2], floatx16 (&dva)[4], con
 #pragma unroll
   for (int i = 0; i < 8; ++i) ob[i] = lds_tr(Dp, ll, 32 * (i & 1) + 16 * ((i >> 1) & 1), 2 + (i >> 2));
 #pragma unroll
-  for (int i = 0; i < 8; ++i) dva[i >> 2] = mfma(oa[i], pp[i & 1][(i >> 1) & 1], dva[i >> 2]);
+  for (int i = 0; i < 8; ++i) dva[i >> 2] = mfma<T>(oa[i], pp[i & 1][(i >> 1) & 1], dva[i >> 2]);
 #pragma unroll
   for (int c = 0; c < 8; ++c) ka[c] = lds_row(Qc, ll, 0, c);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) dva[2 + (i >> 2)] = mfma(ob[i], pp[i & 1][(i >> 1) & 1], dva[2 + (i >> 2)]);
+  for (int i = 0; i < 8; ++i) dva[2 + (i >> 2)] = mfma<T>(ob[i], pp[i & 1][(i >> 1) & 1], dva[2 + (i >> 2)]);
 #pragma unroll
   for (int c = 0; c < 8; ++c) kb[c] = lds_row(Qc, ll, 1, c);
-  s[0] = mfma(ka[0], kf[0], si[0]);
+  s[0] = mfma<T>(ka[0], kf[0], si[0]);
 #pragma unroll
-  for (int c = 1; c < 8; ++c) s[0] = mfma(ka[c], kf[c], s[0]);
-  s[1] = mfma(kb[0], kf[0], si[1]);
+  for (int c = 1; c < 8; ++c) s[0] = mfma<T>(ka[c], kf[c], s[0]);
+  s[1] = mfma<T>(kb[0], kf[0], si[1]);
 #pragma unroll
-  for (int c = 1; c < 8; ++c) s[1] = mfma(kb[c], kf[c], s[1]);
+  for (int c = 1; c < 8; ++c) s[1] = mfma<T>(kb[c], kf[c], s[1]);
 
   mma_phase_order<2>();
 }
 
 // MFMA phase of a dS wave: dK += Q^T dS of the previous tile (Qp, dsf), then
 // dP of the current tile (Dc).
+template <typename T>
 __device__ __forceinline__ void dw_mma(floatx16 (&dp)[2], floatx16 (&dka)[4], const u32x4 (&vf)[8],
                                        const u32x4 (&dsf)[2][2], const bf16_t* Dc, const bf16_t* Qp,
                                        const LaneLds& ll, const float* delta) {
@@ -1176,24 +1205,24 @@ __device__ __forceinline__ void dw_mma(floatx16 (&dp)[2], floatx16 (&dka)[4], co
 #pragma unroll
   for (int i = 0; i < 8; ++i) ob[i] = lds_tr(Qp, ll, 32 * (i & 1) + 16 * ((i >> 1) & 1), 2 + (i >> 2));
 #pragma unroll
-  for (int i = 0; i < 8; ++i) dka[i >> 2] = mfma(oa[i], dsf[i & 1][(i >> 1) & 1], dka[i >> 2]);
+  for (int i = 0; i < 8; ++i) dka[i >> 2] = mfma<T>(oa[i], dsf[i & 1][(i >> 1) & 1], dka[i >> 2]);
 #pragma unroll
   for (int c = 0; c < 8; ++c) ka[c] = lds_row(Dc, ll, 0, c);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) dka[2 + (i >> 2)] = mfma(ob[i], dsf[i & 1][(i >> 1) & 1], dka[2 + (i >> 2)]);
+  for (int i = 0; i < 8; ++i) dka[2 + (i >> 2)] = mfma<T>(ob[i], dsf[i & 1][(i >> 1) & 1], dka[2 + (i >> 2)]);
 #pragma unroll
   for (int c = 0; c < 8; ++c) kb[c] = lds_row(Dc, ll, 1, c);
-  dp[0] = mfma(ka[0], vf[0], di[0]);
+  dp[0] = mfma<T>(ka[0], vf[0], di[0]);
 #pragma unroll
-  for (int c = 1; c < 8; ++c) dp[0] = mfma(ka[c], vf[c], dp[0]);
-  dp[1] = mfma(kb[0], vf[0], di[1]);
+  for (int c = 1; c < 8; ++c) dp[0] = mfma<T>(ka[c], vf[c], dp[0]);
+  dp[1] = mfma<T>(kb[0], vf[0], di[1]);
 #pragma unroll
-  for (int c = 1; c < 8; ++c) dp[1] = mfma(kb[c], vf[c], dp[1]);
+  for (int c = 1; c < 8; ++c) dp[1] = mfma<T>(kb[c], vf[c], dp[1]);
 
   mma_phase_order<8>();
 }
 
-template <bool GATHER>
+template <typename T, bool GATHER>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a, const WorkQ q) {
   __shared__ __attribute__((aligned(1024))) bf16_t Q0[TILE], Q1[TILE], Q2[TILE], Q3[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t D0[TILE], D1[TILE], D2[TILE], D3[TILE];
@@ -1295,7 +1324,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
                      const int* ixc, int* ixn) {
       if (j <= nt) {  // steps past nt (the rounding to 4) would multiply masked tiles and add zeros
         __builtin_amdgcn_s_setprio(1);
-        pw_mma(sc, acc, kf, op, Qc, Dp, ll, Lc, nisl2);
+        pw_mma<T>(sc, acc, kf, op, Qc, Dp, ll, Lc, nisl2);
         __builtin_amdgcn_s_setprio(0);
       }
       block_barrier();
@@ -1323,8 +1352,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
           }
 #pragma unroll
           for (int v = 0; v < 16; ++v) sc[qb][v] = ex2(sc[qb][v] * sl2);
-          op[qb][0] = pack_frag(sc[qb], 0);
-          op[qb][1] = pack_frag(sc[qb], 1);
+          op[qb][0] = pack_frag<T>(sc[qb], 0);
+          op[qb][1] = pack_frag<T>(sc[qb], 1);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) EX[pair][i][lane] = op[i >> 1][i & 1];
@@ -1342,7 +1371,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
     auto dstep = [&](int j, const bf16_t* Dc, const float* Lc, const bf16_t* Qp, bf16_t* Dn, float* Ln) {
       if (j <= nt) {
         __builtin_amdgcn_s_setprio(1);
-        dw_mma(sc, acc, kf, op, Dc, Qp, ll, Lc + BN);
+        dw_mma<T>(sc, acc, kf, op, Dc, Qp, ll, Lc + BN);
         __builtin_amdgcn_s_setprio(0);
       }
       block_barrier();
@@ -1353,12 +1382,12 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
         for (int qb = 0; qb < 2; ++qb) {
           const u32x4 e0 = EX[pair][2 * qb][lane], e1 = EX[pair][2 * qb + 1][lane];
           float pv[16];
-          unpack8(uint4{e0.x, e0.y, e0.z, e0.w}, pv);
-          unpack8(uint4{e1.x, e1.y, e1.z, e1.w}, pv + 8);
+          unpack8_t<T>(uint4{e0.x, e0.y, e0.z, e0.w}, pv);
+          unpack8_t<T>(uint4{e1.x, e1.y, e1.z, e1.w}, pv + 8);
 #pragma unroll
           for (int v = 0; v < 16; ++v) sc[qb][v] = pv[v] * -sc[qb][v];  // P (dP - delta)
-          op[qb][0] = pack_frag(sc[qb], 0);
-          op[qb][1] = pack_frag(sc[qb], 1);
+          op[qb][0] = pack_frag<T>(sc[qb], 0);
+          op[qb][1] = pack_frag<T>(sc[qb], 1);
         }
       } else {
         op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
@@ -1395,9 +1424,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
       int row = my_k, half = hh;
       asm volatile("" : "+v"(row), "+v"(half));
       if (grp == 0)
-        store_rows_bf16(a.dv + ((int64_t)bh * n + row) * LH_D, acc, 1.0f, half);
+        store_rows<T>(a.dv + ((int64_t)bh * n + row) * LH_D, acc, 1.0f, half);
       else
-        store_rows_bf16(a.dk + ((int64_t)bh * n + row) * LH_D, acc, a.scale, half);
+        store_rows<T>(a.dk + ((int64_t)bh * n + row) * LH_D, acc, a.scale, half);
     }
     if (!q.ctr) break;
     have = wq_next(q, a.nq, a.BH, false, next, ++nrun, bh, kblk, wq_s);  // the previous block's copies are waited for there
@@ -1536,10 +1565,10 @@ __device__ __forceinline__ void gla_state_update(floatx16 (&hs)[2], float el, co
     for (int e = 0; e < 4; ++e) {
       const float lo = __uint_as_float(vt[e] << 16) * fv[2 * e];
       const float hi = __uint_as_float(vt[e] & 0xffff0000u) * fv[2 * e + 1];
-      vt[e] = cvt2(lo, hi);
+      vt[e] = cvt2<BF16>(lo, hi);
     }
 #pragma unroll
-    for (int q = 0; q < 2; ++q) hs[q] = mfma(vt, lds_tr(Kt, ll, 16 * kk, sib + q), hs[q]);
+    for (int q = 0; q < 2; ++q) hs[q] = mfma<BF16>(vt, lds_tr(Kt, ll, 16 * kk, sib + q), hs[q]);
   }
 }
 
@@ -1552,7 +1581,7 @@ __device__ __forceinline__ void gla_state_copy(bf16_t (*HT)[TILE], const floatx1
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int j = 32 * sjb + slot_key(v, hh);
-      HT[j >> 6][tile_elem(j & 63, i)] = (bf16_t)(cvt2(hs[q][v], 0.f) & 0xffffu);
+      HT[j >> 6][tile_elem(j & 63, i)] = (bf16_t)(cvt2<BF16>(hs[q][v], 0.f) & 0xffffu);
     }
   }
 }
@@ -1677,7 +1706,7 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
     const int tb = w == 0 ? 0 : 1, sbk = w == 2 ? 1 : 0;
     floatx16 acc = floatx16{};
 #pragma unroll
-    for (int cc = 0; cc < 8; ++cc) acc = mfma(lds_row(Kt[buf], ll, sbk, cc), lds_row(Qt[buf], ll, tb, cc), acc);
+    for (int cc = 0; cc < 8; ++cc) acc = mfma<BF16>(lds_row(Kt[buf], ll, sbk, cc), lds_row(Qt[buf], ll, tb, cc), acc);
     const int t = 32 * tb + l32;
     const float bt = Bw[w][t];
 #pragma unroll
@@ -1691,8 +1720,8 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
         acc[v] = (s <= t && s < nvalid) ? acc[v] * a.scale * ex2(bt - b4[r]) : 0.f;
       }
     }
-    AP[buf][w][0][lane] = pack_frag(acc, 0);
-    AP[buf][w][1][lane] = pack_frag(acc, 1);
+    AP[buf][w][0][lane] = pack_frag<BF16>(acc, 0);
+    AP[buf][w][1][lane] = pack_frag<BF16>(acc, 1);
   };
 
   issue(c0, 0);
@@ -1711,7 +1740,7 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
       // inter-chunk: H^T rows of column block odb against the chunk's queries
 #pragma unroll
       for (int cc = 0; cc < 8; ++cc)
-        oi = mfma(lds_row(HT[odb >> 1], ll, odb & 1, cc), lds_row(Qt[buf], ll, otb, cc), oi);
+        oi = mfma<BF16>(lds_row(HT[odb >> 1], ll, odb & 1, cc), lds_row(Qt[buf], ll, otb, cc), oi);
       // intra-chunk: V^T against the packed A^T blocks of this token block
 #pragma unroll
       for (int sbk = 0; sbk < 2; ++sbk) {
@@ -1719,14 +1748,14 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
         const int blk = otb == 0 ? 0 : 1 + sbk;
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2)
-          oa = mfma(lds_tr(Vt[buf], ll, 32 * sbk + 16 * c2, odb), AP[buf][blk][c2][lane], oa);
+          oa = mfma<BF16>(lds_tr(Vt[buf], ll, 32 * sbk + 16 * c2, odb), AP[buf][blk][c2][lane], oa);
       }
       const float et = Es[buf][32 * otb + l32] * a.scale;
       float ss = 0.f;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const float o = fmaf(oi[v], et, oa[v]);
-        const float ob = __uint_as_float(cvt2(o, 0.f) << 16);  // the bf16 output value
+        const float ob = __uint_as_float(cvt2<BF16>(o, 0.f) << 16);  // the bf16 output value
         ss = fmaf(ob, ob, ss);
       }
       ss += __shfl_xor(ss, 32);
@@ -1740,7 +1769,7 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
     gla_state_copy(HT, hs, sjb, sib, l32, hh);
     if (w == 7 && lane < nvalid) {
       const float ss = (RED[0][lane] + RED[1][lane]) + (RED[2][lane] + RED[3][lane]);
-      const uint32_t nb = cvt2(sqrtf(ss), 0.f) << 16;
+      const uint32_t nb = cvt2<BF16>(sqrtf(ss), 0.f) << 16;
       sq.scores[(int64_t)(64 * c + lane) * a.dil] = __uint_as_float(nb);
     }
     if (c + 1 < c1) prep(c + 1, buf ^ 1);
@@ -1968,17 +1997,17 @@ int query_grid(int BH, int n, hipStream_t st, QPlan& p, WorkQ& q) {
 extern "C" int lh_attn_fwd(const void* q, const void* k, const void* v, int64_t sb, int64_t ss, int64_t sh,
                            const void* qp, const void* kp, const void* vp, int64_t pb, int64_t ps, int64_t ph,
                            int split, const int32_t* indices, int B, int H, int n, int D, float scale, void* out,
-                           float* lse, void* stream) {
+                           float* lse, int dtype, void* stream) {
   AttnArgs a{};
   int rc = fill_rows(a, q, k, v, sb, ss, sh, qp, kp, vp, pb, ps, ph, split, indices, B, H, n, D, scale);
   if (rc) return rc;
-  if (!out || !lse || !al16(out)) return LH_ERR_INVALID_ARG;
+  if (!out || !lse || !al16(out) || !valid_dtype(dtype)) return LH_ERR_INVALID_ARG;
   a.out = (bf16_t*)out; a.lse = lse;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   QPlan p;
   WorkQ wq;
   const int grid = query_grid(a.BH, a.n, st, p, wq);
-  hipLaunchKernelGGL(attn_fwd_kernel<0>, dim3(grid), dim3(64 * QW), 0, st, a, p, wq);
+  LH_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((attn_fwd_kernel<T, 0>), dim3(grid), dim3(64 * QW), 0, st, a, p, wq));
   LH_CHECK_LAUNCH();
   return LH_OK;
 }
@@ -1988,11 +2017,11 @@ namespace {
 int attn_bwd_parts(int parts, const void* q, const void* k, const void* v, int64_t sb, int64_t ss, int64_t sh,
                    const void* qp, const void* kp, const void* vp, int64_t pb, int64_t ps, int64_t ph, int split,
                    const int32_t* indices, int B, int H, int n, int D, float scale, const void* dout,
-                   const float* lse, const float* delta, void* dq, void* dk, void* dv, void* stream) {
+                   const float* lse, const float* delta, void* dq, void* dk, void* dv, int dtype, void* stream) {
   AttnArgs a{};
   int rc = fill_rows(a, q, k, v, sb, ss, sh, qp, kp, vp, pb, ps, ph, split, indices, B, H, n, D, scale);
   if (rc) return rc;
-  if (!dout || !lse || !delta || !al16(dout)) return LH_ERR_INVALID_ARG;
+  if (!dout || !lse || !delta || !al16(dout) || !valid_dtype(dtype)) return LH_ERR_INVALID_ARG;
   if (indices && n < 8) return LH_ERR_UNSUPPORTED;  // gathered rows are indexed 8 at a time
   if ((parts & 1) && (!dk || !dv || !al16(dk) || !al16(dv))) return LH_ERR_INVALID_ARG;
   if ((parts & 2) && (!dq || !al16(dq))) return LH_ERR_INVALID_ARG;
@@ -2004,17 +2033,17 @@ int attn_bwd_parts(int parts, const void* q, const void* k, const void* v, int64
     ak.nq = (a.n + BMK - 1) / BMK;
     WorkQ wq;
     const int grid = wq_grid(ak.nq, ak.BH, st, wq);
-    if (indices)
-      hipLaunchKernelGGL(attn_bwd_dkdv_kernel<true>, dim3(grid), dim3(512), 0, st, ak, wq);
-    else
-      hipLaunchKernelGGL(attn_bwd_dkdv_kernel<false>, dim3(grid), dim3(512), 0, st, ak, wq);
+    LH_DISPATCH_DTYPE(dtype, if (indices) hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, true>), dim3(grid), dim3(512),
+                                                             0, st, ak, wq);
+                      else hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, false>), dim3(grid), dim3(512), 0, st, ak,
+                                              wq));
     LH_CHECK_LAUNCH();
   }
   if (parts & 2) {
     QPlan p;
     WorkQ wq;
     const int grid = query_grid(a.BH, a.n, st, p, wq);
-    hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3(grid), dim3(64 * QW), 0, st, a, p, wq);
+    LH_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL(attn_bwd_dq_kernel<T>, dim3(grid), dim3(64 * QW), 0, st, a, p, wq));
     LH_CHECK_LAUNCH();
   }
   return LH_OK;
@@ -2025,26 +2054,27 @@ extern "C" int lh_attn_bwd(const void* q, const void* k, const void* v, int64_t 
                            const void* qp, const void* kp, const void* vp, int64_t pb, int64_t ps, int64_t ph,
                            int split, const int32_t* indices, int B, int H, int n, int D, float scale,
                            const void* dout, const float* lse, const float* delta, void* dq, void* dk, void* dv,
-                           void* stream) {
+                           int dtype, void* stream) {
   return attn_bwd_parts(3, q, k, v, sb, ss, sh, qp, kp, vp, pb, ps, ph, split, indices, B, H, n, D, scale, dout,
-                        lse, delta, dq, dk, dv, stream);
+                        lse, delta, dq, dk, dv, dtype, stream);
 }
 
 extern "C" int lh_attn_bwd_dkdv(const void* q, const void* k, const void* v, int64_t sb, int64_t ss, int64_t sh,
                                 const void* qp, const void* kp, const void* vp, int64_t pb, int64_t ps, int64_t ph,
                                 int split, const int32_t* indices, int B, int H, int n, int D, float scale,
                                 const void* dout, const float* lse, const float* delta, void* dk, void* dv,
-                                void* stream) {
+                                int dtype, void* stream) {
   return attn_bwd_parts(1, q, k, v, sb, ss, sh, qp, kp, vp, pb, ps, ph, split, indices, B, H, n, D, scale, dout,
-                        lse, delta, nullptr, dk, dv, stream);
+                        lse, delta, nullptr, dk, dv, dtype, stream);
 }
 
 extern "C" int lh_attn_bwd_dq(const void* q, const void* k, const void* v, int64_t sb, int64_t ss, int64_t sh,
                               const void* qp, const void* kp, const void* vp, int64_t pb, int64_t ps, int64_t ph,
                               int split, const int32_t* indices, int B, int H, int n, int D, float scale,
-                              const void* dout, const float* lse, const float* delta, void* dq, void* stream) {
+                              const void* dout, const float* lse, const float* delta, void* dq, int dtype,
+                              void* stream) {
   return attn_bwd_parts(2, q, k, v, sb, ss, sh, qp, kp, vp, pb, ps, ph, split, indices, B, H, n, D, scale, dout,
-                        lse, delta, dq, nullptr, nullptr, stream);
+                        lse, delta, dq, nullptr, nullptr, dtype, stream);
 }
 
 extern "C" int lh_attn_status(int* faults) {
@@ -2088,8 +2118,10 @@ extern "C" int lh_attn_queue_slot(void* stream, void** slot) {
 }
 
 extern "C" int lh_dilated_scores(const void* xq, const void* xk, const void* xv, float* scores_qk, float* scores_kq,
-                                 int B, int S, int H, int D, int dilation, int S_tot, float scale, void* stream) {
+                                 int B, int S, int H, int D, int dilation, int S_tot, float scale, int dtype,
+                                 void* stream) {
   if (D != LH_D) return LH_ERR_UNSUPPORTED;
+  if (!valid_dtype(dtype)) return LH_ERR_INVALID_ARG;
   if (!xq || !xk || !xv || !scores_qk || !scores_kq || dilation <= 0 || S <= 0 || S % dilation || S_tot < S)
     return LH_ERR_INVALID_ARG;
   const int n = S / dilation;
@@ -2108,7 +2140,7 @@ extern "C" int lh_dilated_scores(const void* xq, const void* xk, const void* xv,
     QPlan p;
     WorkQ wq;
     const int grid = query_grid(a.BH, a.n, st, p, wq);
-    hipLaunchKernelGGL(attn_fwd_kernel<1>, dim3(grid), dim3(64 * QW), 0, st, a, p, wq);
+    LH_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL((attn_fwd_kernel<T, 1>), dim3(grid), dim3(64 * QW), 0, st, a, p, wq));
     LH_CHECK_LAUNCH();
   }
   return LH_OK;

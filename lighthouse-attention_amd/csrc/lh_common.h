@@ -46,6 +46,62 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
   return v;
 }
 
+// ---------------------------------------------------------------------------
+// Element types of the row kernels (layer inputs, pyramid, attention rows and
+// outputs): bf16, what the reference configs run, and fp16.  Both are 16-bit;
+// arithmetic is fp32 with one rounding per stored value (round to nearest
+// even, as torch's casts).  pack2(lo, hi) rounds two floats into one word,
+// lo/hi widen the low/high half of a word.
+// ---------------------------------------------------------------------------
+typedef _Float16 lh_f16x2 __attribute__((ext_vector_type(2)));
+struct BF16 {
+  static constexpr int code = LH_DTYPE_BF16;
+  __device__ static __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  __device__ static __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  __device__ static __forceinline__ uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
+};
+struct F16 {
+  static constexpr int code = LH_DTYPE_F16;
+  __device__ static __forceinline__ float lo(uint32_t w) { return (float)__builtin_bit_cast(lh_f16x2, w).x; }
+  __device__ static __forceinline__ float hi(uint32_t w) { return (float)__builtin_bit_cast(lh_f16x2, w).y; }
+  __device__ static __forceinline__ uint32_t pack2(float a, float b) {
+    const lh_f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, lh_f16x2));
+  }
+};
+
+// x rounded to the element type and widened back (a stored-then-loaded value)
+template <typename T>
+__device__ __forceinline__ float round_to(float x) { return T::lo(T::pack2(x, 0.f)); }
+
+template <typename T>
+__device__ __forceinline__ void unpack8_t(const uint4 v, float* f) {
+  f[0] = T::lo(v.x); f[1] = T::hi(v.x); f[2] = T::lo(v.y); f[3] = T::hi(v.y);
+  f[4] = T::lo(v.z); f[5] = T::hi(v.z); f[6] = T::lo(v.w); f[7] = T::hi(v.w);
+}
+
+template <typename T>
+__device__ __forceinline__ uint4 pack8_t(const float* f) {
+  uint4 v;
+  v.x = T::pack2(f[0], f[1]); v.y = T::pack2(f[2], f[3]);
+  v.z = T::pack2(f[4], f[5]); v.w = T::pack2(f[6], f[7]);
+  return v;
+}
+
+// Launch helper: F(tag) for the element type named by a dtype code.
+#define LH_DISPATCH_DTYPE(dtype, ...)                         \
+  do {                                                       \
+    if ((dtype) == LH_DTYPE_F16) {                           \
+      using T = F16;                                         \
+      __VA_ARGS__;                                           \
+    } else {                                                 \
+      using T = BF16;                                        \
+      __VA_ARGS__;                                           \
+    }                                                        \
+  } while (0)
+
+static inline bool valid_dtype(int dtype) { return dtype == LH_DTYPE_BF16 || dtype == LH_DTYPE_F16; }
+
 // 16-byte store with the nontemporal hint (a vector store, `global_store ... nt`):
 // for outputs that no kernel of the same pass reads back soon.  Their lines then
 // do not stay dirty in the 256 MB last-level cache, where the next streaming

@@ -2,7 +2,8 @@
 //
 // Forward restates DialatedLighthouseNormScorer.forward
 // (src/lighthouse_selection.py:589-616): base scores are the L2 norms of q and
-// k rows, rounded to bf16 like torch's bf16 `norm`; level j = 1..L-1 rows are
+// k rows, rounded to the row type (bf16 or fp16) like torch's `norm` of such
+// rows; level j = 1..L-1 rows are
 // the means of p^j consecutive base rows (fp32 sum, one rounding), and level-j
 // scores are maxima of the base scores over the same span.  One pass streams
 // xq/xk/xv once: 16 lanes own one (b, span, head) unit, 8 bf16 each, and walk
@@ -39,24 +40,24 @@ constexpr int PYR_CHUNK = 4;  // base tokens whose loads are issued together
 // values kept), and make its base scores: the bf16-rounded L2 norms of q and k
 // (every lane of the 16-lane group gets them), or the given ones (GIVEN: sq, sk
 // on entry).
-template <bool GIVEN, bool ROPE>
+template <typename T, bool GIVEN, bool ROPE>
 __device__ __forceinline__ void pyr_token(const PyrArgs& a, int b, int h, int l16, size_t srow, int t,
                                           const uint4 xq, const uint4 xk, const uint4 xv, float* fq, float* fk,
                                           float* fv, float& sq, float& sk) {
-  unpack8(xq, fq);
-  unpack8(xk, fk);
-  unpack8(xv, fv);
+  unpack8_t<T>(xq, fq);
+  unpack8_t<T>(xk, fk);
+  unpack8_t<T>(xv, fv);
   if (ROPE) {
     float4 c01, c23;
     rope_freqs8(a.fs, t, LH_D, 8 * l16, c01, c23);
     rope_rotate8<true>(fq, c01, c23);
     rope_rotate8<true>(fk, c01, c23);
-    const uint4 wq = pack8(fq), wk = pack8(fk);
+    const uint4 wq = pack8_t<T>(fq), wk = pack8_t<T>(fk);
     const int64_t ro = (int64_t)b * a.rb + (int64_t)t * a.rs + (int64_t)h * a.rh + 8 * l16;
     *reinterpret_cast<uint4*>(a.rq + ro) = wq;
     *reinterpret_cast<uint4*>(a.rk + ro) = wk;
-    unpack8(wq, fq);
-    unpack8(wk, fk);
+    unpack8_t<T>(wq, fq);
+    unpack8_t<T>(wk, fk);
   }
   if (!GIVEN) {
     float pq = 0.f, pk = 0.f;
@@ -64,8 +65,8 @@ __device__ __forceinline__ void pyr_token(const PyrArgs& a, int b, int h, int l1
     for (int e = 0; e < 8; ++e) { pq = fmaf(fq[e], fq[e], pq); pk = fmaf(fk[e], fk[e], pk); }
 #pragma unroll
     for (int m = 1; m < 16; m <<= 1) { pq += __shfl_xor(pq, m, 16); pk += __shfl_xor(pk, m, 16); }
-    sq = bf16_to_f32(f32_to_bf16(sqrtf(pq)));
-    sk = bf16_to_f32(f32_to_bf16(sqrtf(pk)));
+    sq = round_to<T>(sqrtf(pq));
+    sk = round_to<T>(sqrtf(pk));
   }
 }
 
@@ -73,7 +74,7 @@ __device__ __forceinline__ void pyr_token(const PyrArgs& a, int b, int h, int l1
 // position's angles, rounded to bf16 and written to rq / rk, and the norms and
 // means below are taken of those rounded rows, exactly as if the rotated rows
 // had been stored first and read back.
-template <int NL, bool GIVEN, bool ROPE>
+template <typename T, int NL, bool GIVEN, bool ROPE>
 __global__ __launch_bounds__(256) void pyramid_fwd_kernel(const PyrArgs a) {
   const int tid = threadIdx.x;
   const int u = blockIdx.x * 16 + (tid >> 4);
@@ -101,7 +102,7 @@ __global__ __launch_bounds__(256) void pyramid_fwd_kernel(const PyrArgs a) {
   auto token = [&](int t, const uint4 xq, const uint4 xk, const uint4 xv, float sq, float sk)
       __attribute__((always_inline)) {
     float fq[8], fk[8], fv[8];
-    pyr_token<GIVEN, ROPE>(a, b, h, l16, srow, t, xq, xk, xv, fq, fk, fv, sq, sk);
+    pyr_token<T, GIVEN, ROPE>(a, b, h, l16, srow, t, xq, xk, xv, fq, fk, fv, sq, sk);
     if (!GIVEN) {
       // base scores leave 16 tokens at a time: lane j keeps token t0 + 16 i + j,
       // and the group stores them as one contiguous 64-byte run per tensor
@@ -127,13 +128,13 @@ __global__ __launch_bounds__(256) void pyramid_fwd_kernel(const PyrArgs a) {
         const int64_t prow = (int64_t)b * a.pb + (int64_t)(a.off[lvl] - a.S + node) * a.ps + (int64_t)h * a.ph + 8 * l16;
 #pragma unroll
         for (int e = 0; e < 8; ++e) mo[e] = accq[l][e] * inv_c;
-        *reinterpret_cast<uint4*>(a.pq + prow) = pack8(mo);
+        *reinterpret_cast<uint4*>(a.pq + prow) = pack8_t<T>(mo);
 #pragma unroll
         for (int e = 0; e < 8; ++e) mo[e] = acck[l][e] * inv_c;
-        *reinterpret_cast<uint4*>(a.pk + prow) = pack8(mo);
+        *reinterpret_cast<uint4*>(a.pk + prow) = pack8_t<T>(mo);
 #pragma unroll
         for (int e = 0; e < 8; ++e) mo[e] = accv[l][e] * inv_c;
-        *reinterpret_cast<uint4*>(a.pv + prow) = pack8(mo);
+        *reinterpret_cast<uint4*>(a.pv + prow) = pack8_t<T>(mo);
         if (l16 == 0) {
           a.sqk[srow + a.off[lvl] + node] = mq[l];
           a.skq[srow + a.off[lvl] + node] = mk[l];
@@ -194,7 +195,7 @@ struct PyrBwdArgs {
 // memory round trips instead of two per level.  ROPE: the q and k sums are
 // the gradients of rotated rows; they are rotated back (the adjoint of the
 // forward rotation) in fp32 before the one rounding.
-template <int NL, bool ROPE>
+template <typename T, int NL, bool ROPE>
 __global__ __launch_bounds__(256) void pyramid_bwd_kernel(const PyrBwdArgs a) {
   const int tid = threadIdx.x;
   const long long blk = xcd_run(blockIdx.x, gridDim.x, 32);
@@ -227,13 +228,13 @@ __global__ __launch_bounds__(256) void pyramid_bwd_kernel(const PyrBwdArgs a) {
   for (int l = 0; l < NL; ++l) {
     const float w = 1.0f / (float)(1 << (l * a.shift));
     float g[8];
-    unpack8(gq[l], g);
+    unpack8_t<T>(gq[l], g);
 #pragma unroll
     for (int e = 0; e < 8; ++e) fq[e] = fmaf(g[e], w, fq[e]);
-    unpack8(gk[l], g);
+    unpack8_t<T>(gk[l], g);
 #pragma unroll
     for (int e = 0; e < 8; ++e) fk[e] = fmaf(g[e], w, fk[e]);
-    unpack8(gv[l], g);
+    unpack8_t<T>(gv[l], g);
 #pragma unroll
     for (int e = 0; e < 8; ++e) fv[e] = fmaf(g[e], w, fv[e]);
   }
@@ -244,20 +245,20 @@ __global__ __launch_bounds__(256) void pyramid_bwd_kernel(const PyrBwdArgs a) {
     rope_rotate8<false>(fk, c01, c23);
   }
   const int64_t o = (int64_t)b * a.ob + (int64_t)t * a.os + (int64_t)h * a.oh + 8 * l16;
-  if (a.dq) store16_nt(a.dq + o, pack8(fq));
-  if (a.dk) store16_nt(a.dk + o, pack8(fk));
-  if (a.dv) store16_nt(a.dv + o, pack8(fv));
+  if (a.dq) store16_nt(a.dq + o, pack8_t<T>(fq));
+  if (a.dk) store16_nt(a.dk + o, pack8_t<T>(fk));
+  if (a.dv) store16_nt(a.dv + o, pack8_t<T>(fv));
 }
 
-template <int NL>
+template <typename T, int NL>
 int launch_fwd(const PyrArgs& a, bool given, hipStream_t st) {
   const int blocks = (a.units + 15) / 16;
   if (a.fs)
-    hipLaunchKernelGGL((pyramid_fwd_kernel<NL, false, true>), dim3(blocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((pyramid_fwd_kernel<BF16, NL, false, true>), dim3(blocks), dim3(256), 0, st, a);
   else if (given)
-    hipLaunchKernelGGL((pyramid_fwd_kernel<NL, true, false>), dim3(blocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((pyramid_fwd_kernel<T, NL, true, false>), dim3(blocks), dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((pyramid_fwd_kernel<NL, false, false>), dim3(blocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((pyramid_fwd_kernel<T, NL, false, false>), dim3(blocks), dim3(256), 0, st, a);
   LH_CHECK_LAUNCH();
   return LH_OK;
 }
@@ -272,8 +273,9 @@ int pyramid_fwd_impl(const void* xq, const void* xk, const void* xv, int64_t sb,
                      const float* freqs, void* rq, void* rk, int64_t rb, int64_t rs, int64_t rh,
                      void* pq, void* pk, void* pv, int64_t pb, int64_t ps, int64_t ph,
                      float* scores_qk, float* scores_kq, int B, int S, int H, int D, int L, int p,
-                     bool given, void* stream) {
+                     bool given, int dtype, void* stream) {
   if (D != LH_D) return LH_ERR_UNSUPPORTED;
+  if (!valid_dtype(dtype) || (freqs && dtype != LH_DTYPE_BF16)) return LH_ERR_INVALID_ARG;
   if (!xq || !xk || !xv || !scores_qk || !scores_kq || B <= 0 || H <= 0 || S <= 0) return LH_ERR_INVALID_ARG;
   const int shift = ilog2_exact(p);
   if (shift <= 0 || L < 1) return LH_ERR_INVALID_ARG;
@@ -303,36 +305,39 @@ int pyramid_fwd_impl(const void* xq, const void* xk, const void* xv, int64_t sb,
   a.units = (int)units;
   for (int l = 1; l <= L; ++l) { a.off[l] = g.off[l]; a.len[l] = g.len[l]; }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  switch (L - 1) {
-    case 0: return launch_fwd<0>(a, given, st);
-    case 1: return launch_fwd<1>(a, given, st);
-    case 2: return launch_fwd<2>(a, given, st);
-    case 3: return launch_fwd<3>(a, given, st);
-    case 4: return launch_fwd<4>(a, given, st);
-    default: return launch_fwd<5>(a, given, st);
-  }
+  int rc = LH_OK;
+  LH_DISPATCH_DTYPE(dtype, switch (L - 1) {
+    case 0: rc = launch_fwd<T, 0>(a, given, st); break;
+    case 1: rc = launch_fwd<T, 1>(a, given, st); break;
+    case 2: rc = launch_fwd<T, 2>(a, given, st); break;
+    case 3: rc = launch_fwd<T, 3>(a, given, st); break;
+    case 4: rc = launch_fwd<T, 4>(a, given, st); break;
+    default: rc = launch_fwd<T, 5>(a, given, st); break;
+  });
+  return rc;
 }
 
-template <bool ROPE>
+template <typename T, bool ROPE>
 void launch_bwd(const PyrBwdArgs& a, dim3 grid, hipStream_t st) {
   const dim3 blk(256);
   switch (a.L) {
-    case 1: hipLaunchKernelGGL((pyramid_bwd_kernel<1, ROPE>), grid, blk, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((pyramid_bwd_kernel<2, ROPE>), grid, blk, 0, st, a); break;
-    case 3: hipLaunchKernelGGL((pyramid_bwd_kernel<3, ROPE>), grid, blk, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((pyramid_bwd_kernel<4, ROPE>), grid, blk, 0, st, a); break;
-    case 5: hipLaunchKernelGGL((pyramid_bwd_kernel<5, ROPE>), grid, blk, 0, st, a); break;
-    case 6: hipLaunchKernelGGL((pyramid_bwd_kernel<6, ROPE>), grid, blk, 0, st, a); break;
-    case 7: hipLaunchKernelGGL((pyramid_bwd_kernel<7, ROPE>), grid, blk, 0, st, a); break;
-    default: hipLaunchKernelGGL((pyramid_bwd_kernel<8, ROPE>), grid, blk, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((pyramid_bwd_kernel<T, 1, ROPE>), grid, blk, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((pyramid_bwd_kernel<T, 2, ROPE>), grid, blk, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((pyramid_bwd_kernel<T, 3, ROPE>), grid, blk, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((pyramid_bwd_kernel<T, 4, ROPE>), grid, blk, 0, st, a); break;
+    case 5: hipLaunchKernelGGL((pyramid_bwd_kernel<T, 5, ROPE>), grid, blk, 0, st, a); break;
+    case 6: hipLaunchKernelGGL((pyramid_bwd_kernel<T, 6, ROPE>), grid, blk, 0, st, a); break;
+    case 7: hipLaunchKernelGGL((pyramid_bwd_kernel<T, 7, ROPE>), grid, blk, 0, st, a); break;
+    default: hipLaunchKernelGGL((pyramid_bwd_kernel<T, 8, ROPE>), grid, blk, 0, st, a); break;
   }
 }
 
 int pyramid_bwd_impl(const void* gq, const void* gk, const void* gv, int64_t gb, int64_t gh, int64_t gs,
                      const int32_t* inverse, const float* freqs, void* dxq, void* dxk, void* dxv, int64_t ob,
-                     int64_t os, int64_t oh, int B, int S, int H, int D, int L, int p, void* stream) {
+                     int64_t os, int64_t oh, int B, int S, int H, int D, int L, int p, int dtype, void* stream) {
   if (D != LH_D) return LH_ERR_UNSUPPORTED;
   if (B <= 0 || H <= 0 || S <= 0 || L < 1 || L > 8) return LH_ERR_INVALID_ARG;
+  if (!valid_dtype(dtype) || (freqs && dtype != LH_DTYPE_BF16)) return LH_ERR_INVALID_ARG;
   const int shift = ilog2_exact(p);
   if (shift <= 0) return LH_ERR_INVALID_ARG;
   if ((gq != nullptr) != (dxq != nullptr) || (gk != nullptr) != (dxk != nullptr) || (gv != nullptr) != (dxv != nullptr))
@@ -356,9 +361,9 @@ int pyramid_bwd_impl(const void* gq, const void* gk, const void* gv, int64_t gb,
   if (blocks > 2147483647LL) return LH_ERR_UNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (freqs)
-    launch_bwd<true>(a, dim3((unsigned)blocks), st);
+    launch_bwd<BF16, true>(a, dim3((unsigned)blocks), st);
   else
-    launch_bwd<false>(a, dim3((unsigned)blocks), st);
+    LH_DISPATCH_DTYPE(dtype, launch_bwd<T, false>(a, dim3((unsigned)blocks), st));
   LH_CHECK_LAUNCH();
   return LH_OK;
 }
@@ -368,9 +373,9 @@ int pyramid_bwd_impl(const void* gq, const void* gk, const void* gv, int64_t gb,
 extern "C" int lh_pyramid_fwd(const void* xq, const void* xk, const void* xv, int64_t sb, int64_t ss, int64_t sh,
                               void* pq, void* pk, void* pv, int64_t pb, int64_t ps, int64_t ph,
                               float* scores_qk, float* scores_kq, int B, int S, int H, int D, int L, int p,
-                              int base_scores_given, void* stream) {
+                              int base_scores_given, int dtype, void* stream) {
   return pyramid_fwd_impl(xq, xk, xv, sb, ss, sh, nullptr, nullptr, nullptr, 0, 0, 0, pq, pk, pv, pb, ps, ph,
-                          scores_qk, scores_kq, B, S, H, D, L, p, base_scores_given != 0, stream);
+                          scores_qk, scores_kq, B, S, H, D, L, p, base_scores_given != 0, dtype, stream);
 }
 
 extern "C" int lh_rope_pyramid_fwd(const void* xq, const void* xk, const void* xv, int64_t sb, int64_t ss,
@@ -380,15 +385,15 @@ extern "C" int lh_rope_pyramid_fwd(const void* xq, const void* xk, const void* x
                                    void* stream) {
   if (!freqs) return LH_ERR_INVALID_ARG;
   return pyramid_fwd_impl(xq, xk, xv, sb, ss, sh, freqs, rq, rk, rb, rs, rh, pq, pk, pv, pb, ps, ph, scores_qk,
-                          scores_kq, B, S, H, D, L, p, false, stream);
+                          scores_kq, B, S, H, D, L, p, false, LH_DTYPE_BF16, stream);
 }
 
 extern "C" int lh_pyramid_bwd(const void* gq, const void* gk, const void* gv, int64_t gb, int64_t gh, int64_t gs,
                               const int32_t* inverse, void* dxq, void* dxk, void* dxv, int B, int S, int H, int D,
-                              int L, int p, void* stream) {
+                              int L, int p, int dtype, void* stream) {
   const int64_t oh = D, os = (int64_t)H * D, ob = (int64_t)S * os;
   return pyramid_bwd_impl(gq, gk, gv, gb, gh, gs, inverse, nullptr, dxq, dxk, dxv, ob, os, oh, B, S, H, D, L, p,
-                          stream);
+                          dtype, stream);
 }
 
 extern "C" int lh_pyramid_rope_bwd(const void* gq, const void* gk, const void* gv, int64_t gb, int64_t gh,
@@ -397,5 +402,5 @@ extern "C" int lh_pyramid_rope_bwd(const void* gq, const void* gk, const void* g
                                    int p, void* stream) {
   if (!freqs) return LH_ERR_INVALID_ARG;
   return pyramid_bwd_impl(gq, gk, gv, gb, gh, gs, inverse, freqs, dxq, dxk, dxv, ob, os, oh, B, S, H, D, L, p,
-                          stream);
+                          LH_DTYPE_BF16, stream);
 }

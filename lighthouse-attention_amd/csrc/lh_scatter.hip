@@ -9,7 +9,8 @@
 //
 // Backward restates _scatter_fanout_bwd_kernel (:462-514): each selected row
 // sums dout over its span.  The same pass forms delta = rowsum(dattn * o) for
-// the attention backward from the bf16-rounded dattn, as SDPA's backward does.
+// the attention backward from the rounded dattn, as SDPA's backward does.
+// Rows are bf16 or fp16 (the element type T), sums fp32.
 #include "lh_common.h"
 
 namespace {
@@ -41,7 +42,7 @@ constexpr int SCAT_RUN = 16;
 // levels' inverse lookups are issued first, then all row loads, so a group
 // has SF_ROWS * NL loads in flight across two dependent round trips.
 constexpr int SF_ROWS = 2;
-template <int NL, int R>
+template <typename T, int NL, int R>
 __global__ __launch_bounds__(256) void scatter_fwd_kernel(const ScatArgs a) {
   const int tid = threadIdx.x;
   const int l16 = tid & 15;
@@ -79,12 +80,12 @@ __global__ __launch_bounds__(256) void scatter_fwd_kernel(const ScatArgs a) {
     for (int l = 0; l < NL; ++l) {
       if (s[r][l] < 0) continue;  // keeps the fp32 sum of exactly the present terms
       float f[8];
-      unpack8(v[r][l], f);
+      unpack8_t<T>(v[r][l], f);
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] += f[e];
     }
     const int b = (int)(bhr[r] / a.H), h = (int)(bhr[r] % a.H);
-    store16_nt(a.dst + b * a.sb + h * a.sh + (int64_t)tr[r] * a.st + 8 * l16, pack8(acc));
+    store16_nt(a.dst + b * a.sb + h * a.sh + (int64_t)tr[r] * a.st + 8 * l16, pack8_t<T>(acc));
   }
 }
 
@@ -94,6 +95,7 @@ __global__ __launch_bounds__(256) void scatter_fwd_kernel(const ScatArgs a) {
 // different times, and one-wave blocks free their slots soonest); XCD runs
 // stay 256 rows long.
 constexpr int SB_ROWS = 4;
+template <typename T>
 __global__ __launch_bounds__(16 * SB_ROWS) void scatter_bwd_kernel(const ScatArgs a) {
   const int tid = threadIdx.x;
   const long long row = xcd_run(blockIdx.x, gridDim.x, SCAT_RUN * 16 / SB_ROWS) * SB_ROWS + (tid >> 4);
@@ -122,18 +124,18 @@ __global__ __launch_bounds__(16 * SB_ROWS) void scatter_bwd_kernel(const ScatArg
       for (int u = 0; u < 8; ++u) {
         if (t + u >= stop) break;  // same left-to-right fp32 sum as one row at a time
         float f[8];
-        unpack8(v[u], f);
+        unpack8_t<T>(v[u], f);
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] += f[e];
       }
     }
   }
-  const uint4 packed = pack8(acc);
+  const uint4 packed = pack8_t<T>(acc);
   *reinterpret_cast<uint4*>(a.dst + (size_t)row * LH_D + 8 * l16) = packed;
   if (a.delta) {
     float g[8], o[8];
-    unpack8(packed, g);
-    unpack8(ov, o);
+    unpack8_t<T>(packed, g);
+    unpack8_t<T>(ov, o);
     float d = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) d = fmaf(g[e], o[e], d);
@@ -158,9 +160,10 @@ int fill(ScatArgs& a, int S, int S_out, int n, int L, int p, int B, int H, int64
 }  // namespace
 
 extern "C" int lh_scatter_fwd(const void* attn, const int32_t* inverse, void* out, int64_t ob, int64_t oh,
-                              int64_t os, int B, int H, int S, int S_out, int n, int D, int L, int p, void* stream) {
+                              int64_t os, int B, int H, int S, int S_out, int n, int D, int L, int p, int dtype,
+                              void* stream) {
   if (D != LH_D) return LH_ERR_UNSUPPORTED;
-  if (!attn || !inverse || !out || ((uintptr_t)out & 15)) return LH_ERR_INVALID_ARG;
+  if (!attn || !inverse || !out || ((uintptr_t)out & 15) || !valid_dtype(dtype)) return LH_ERR_INVALID_ARG;
   ScatArgs a{};
   int rc = fill(a, S, S_out, n, L, p, B, H, ob, oh, os);
   if (rc) return rc;
@@ -170,25 +173,26 @@ extern "C" int lh_scatter_fwd(const void* attn, const int32_t* inverse, void* ou
   if (blocks > 2147483647LL) return LH_ERR_UNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)blocks), blk(256);
-  switch (L) {
-    case 1: hipLaunchKernelGGL((scatter_fwd_kernel<1, SF_ROWS>), grid, blk, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((scatter_fwd_kernel<2, SF_ROWS>), grid, blk, 0, st, a); break;
-    case 3: hipLaunchKernelGGL((scatter_fwd_kernel<3, SF_ROWS>), grid, blk, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((scatter_fwd_kernel<4, SF_ROWS>), grid, blk, 0, st, a); break;
-    case 5: hipLaunchKernelGGL((scatter_fwd_kernel<5, SF_ROWS>), grid, blk, 0, st, a); break;
-    case 6: hipLaunchKernelGGL((scatter_fwd_kernel<6, SF_ROWS>), grid, blk, 0, st, a); break;
-    case 7: hipLaunchKernelGGL((scatter_fwd_kernel<7, SF_ROWS>), grid, blk, 0, st, a); break;
-    default: hipLaunchKernelGGL((scatter_fwd_kernel<8, SF_ROWS>), grid, blk, 0, st, a); break;
-  }
+  LH_DISPATCH_DTYPE(dtype, switch (L) {
+    case 1: hipLaunchKernelGGL((scatter_fwd_kernel<T, 1, SF_ROWS>), grid, blk, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((scatter_fwd_kernel<T, 2, SF_ROWS>), grid, blk, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((scatter_fwd_kernel<T, 3, SF_ROWS>), grid, blk, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((scatter_fwd_kernel<T, 4, SF_ROWS>), grid, blk, 0, st, a); break;
+    case 5: hipLaunchKernelGGL((scatter_fwd_kernel<T, 5, SF_ROWS>), grid, blk, 0, st, a); break;
+    case 6: hipLaunchKernelGGL((scatter_fwd_kernel<T, 6, SF_ROWS>), grid, blk, 0, st, a); break;
+    case 7: hipLaunchKernelGGL((scatter_fwd_kernel<T, 7, SF_ROWS>), grid, blk, 0, st, a); break;
+    default: hipLaunchKernelGGL((scatter_fwd_kernel<T, 8, SF_ROWS>), grid, blk, 0, st, a); break;
+  });
   LH_CHECK_LAUNCH();
   return LH_OK;
 }
 
 extern "C" int lh_scatter_bwd(const void* dout, int64_t db, int64_t dh, int64_t ds, const int32_t* indices,
                               const void* o, void* dattn, float* delta, int B, int H, int S, int S_out, int n, int D,
-                              int L, int p, void* stream) {
+                              int L, int p, int dtype, void* stream) {
   if (D != LH_D) return LH_ERR_UNSUPPORTED;
-  if (!dout || !indices || !dattn || ((o == nullptr) != (delta == nullptr)) || ((uintptr_t)dout & 15))
+  if (!dout || !indices || !dattn || ((o == nullptr) != (delta == nullptr)) || ((uintptr_t)dout & 15) ||
+      !valid_dtype(dtype))
     return LH_ERR_INVALID_ARG;
   ScatArgs a{};
   int rc = fill(a, S, S_out, n, L, p, B, H, db, dh, ds);
@@ -198,8 +202,8 @@ extern "C" int lh_scatter_bwd(const void* dout, int64_t db, int64_t dh, int64_t 
   if (a.rows == 0) return LH_OK;
   const long long blocks = (a.rows + SB_ROWS - 1) / SB_ROWS;
   if (blocks > 2147483647LL) return LH_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(scatter_bwd_kernel, dim3((unsigned)blocks), dim3(16 * SB_ROWS), 0,
-                     reinterpret_cast<hipStream_t>(stream), a);
+  LH_DISPATCH_DTYPE(dtype, hipLaunchKernelGGL(scatter_bwd_kernel<T>, dim3((unsigned)blocks), dim3(16 * SB_ROWS), 0,
+                                              reinterpret_cast<hipStream_t>(stream), a));
   LH_CHECK_LAUNCH();
   return LH_OK;
 }

@@ -57,7 +57,7 @@ class _DenseCausalFn(torch.autograd.Function):
 
 @graph_break
 def dense_causal_attention(q, k, v):
-    """Causal softmax attention, scale 1/sqrt(D): ``q, k, v`` bf16 ``[B, H, S, D]``
+    """Causal softmax attention, scale 1/sqrt(D): ``q, k, v`` bf16 or fp16 ``[B, H, S, D]``
     (any batch/head/seq strides, D contiguous) -> ``[B, H, S, D]``.  D < 128 (a
     multiple of 8) runs zero-padded to the kernels' 128 with scale 1/sqrt(D)."""
     D = q.shape[-1]
@@ -66,8 +66,9 @@ def dense_causal_attention(q, k, v):
     if not (q.shape == k.shape == v.shape):
         raise ValueError("q, k and v must have the same shape")
     for t in (q, k, v):
-        if t.dtype != torch.bfloat16:
-            raise TypeError("the native attention computes in bfloat16; got " + str(t.dtype))
+        if t.dtype not in N.ROW_DTYPES or t.dtype != q.dtype:
+            raise TypeError("the native attention computes in bfloat16 or float16 (one dtype for q, k, v); got "
+                            + ", ".join(str(x.dtype) for x in (q, k, v)))
     if D < N.D_SUPPORTED:
         q, k, v = (torch.nn.functional.pad(x, (0, N.D_SUPPORTED - D)) for x in (q, k, v))
         return _DenseCausalFn.apply(q, k, v, D ** -0.5)[..., :D]

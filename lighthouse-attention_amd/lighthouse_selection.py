@@ -230,6 +230,20 @@ class _LighthouseLayerFn(torch.autograd.Function):
         return dx + (None,) * 9  # the gate gets no gradient: the scores only feed the selection
 
 
+def _need_layer_dtype(*ts):
+    """The layer's kernels read and write bf16 or fp16 rows (all three inputs of
+    one type; selection, softmax statistics and sums stay fp32).  The reference
+    path is dtype-generic (``src/lighthouse_selection.py:522,528,559,562``);
+    float32 inputs are refused rather than silently downcast: cast them (or run
+    under autocast) to bfloat16 or float16 first."""
+    for t in ts:
+        if t.dtype not in N.ROW_DTYPES:
+            raise TypeError("the native layer computes in bfloat16 or float16 (cast float32 inputs first, "
+                            "e.g. under autocast); got " + str(t.dtype))
+    if len({t.dtype for t in ts}) > 1:
+        raise TypeError("xq, xk and xv must share a dtype; got " + ", ".join(str(t.dtype) for t in ts))
+
+
 def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, topk: int = 1024,
                      tie_break: str = "reference", strict: bool = True, dilation: int = 0,
                      seq_major: bool = False, gk=None):
@@ -252,14 +266,14 @@ def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, t
         raise ValueError(f"head_dim must be a multiple of 8 and at most {N.D_SUPPORTED}, got {D}")
     if not (xq.shape == xk.shape == xv.shape):
         raise AssertionError("xq, xk and xv must have the same shape (n_kv_heads == n_heads)")
-    for t in (xq, xk, xv):
-        if t.dtype != torch.bfloat16:
-            raise TypeError("the native layer computes in bfloat16; got " + str(t.dtype))
+    _need_layer_dtype(xq, xk, xv)
     if tie_break not in N.TIE_MODES:
         raise ValueError(f"tie_break must be one of {sorted(N.TIE_MODES)}, got {tie_break!r}")
     if gk is not None:
         if dilation <= 0:
             raise ValueError("the GLA scorer needs dilation >= 1")
+        if xq.dtype != torch.bfloat16:
+            raise TypeError("the GLA scorer's kernels read bfloat16 rows; got " + str(xq.dtype))
         gk = gk.detach()
     scale = None
     if D < N.D_SUPPORTED:
@@ -604,7 +618,7 @@ def scatter_to_base_sequence(attn_out, indices_hp, rank_ids_hp, N_shard: int, N_
 
     Only the single-shard form is built: ``rank_ids_hp`` must be all zeros,
     which is what every reference caller passes (:817, :1045-1046).
-    ``attn_out`` must be bfloat16 (``TypeError`` otherwise).  The fan-out is
+    ``attn_out`` must be bfloat16 or float16 (``TypeError`` otherwise).  The fan-out is
     gather-formulated, so every (b, h) must name each pyramid row at most once;
     ``validate`` (default) checks that and the index range on the device and
     raises ``IndexError`` (one stream synchronisation); entries of -1 are empty

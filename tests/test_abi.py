@@ -94,20 +94,30 @@ def test_host_validation_rejects_before_launch(pkg):
     null = ctypes.c_void_p(0)
     # unsupported head dim, null pointers, bad tie mode: all refused on the host
     assert lib.lh_attn_fwd(null, null, null, 0, 0, 0, null, null, null, 0, 0, 0, 0, null,
-                           1, 1, 128, 64, ctypes.c_float(0.1), null, null, null) == 4
+                           1, 1, 128, 64, ctypes.c_float(0.1), null, null, 0, null) == 4
     assert lib.lh_attn_fwd(null, null, null, 0, 0, 0, null, null, null, 0, 0, 0, 0, null,
-                           1, 1, 128, 128, ctypes.c_float(0.1), null, null, null) == 1
+                           1, 1, 128, 128, ctypes.c_float(0.1), null, null, 0, null) == 1
     assert lib.lh_select_topk(null, null, null, null, 1, 1, 4096, 3, 4, 256, 0, 1, null) == 1
     assert lib.lh_pyramid_fwd(null, null, null, 0, 0, 0, null, null, null, 0, 0, 0, null, null,
-                              1, 1024, 1, 128, 3, 4, 0, null) == 1
-    assert lib.lh_scatter_fwd(null, null, null, 0, 0, 0, 1, 1, 1024, 1024, 10, 64, 3, 4, null) == 4
+                              1, 1024, 1, 128, 3, 4, 0, 0, null) == 1
+    assert lib.lh_scatter_fwd(null, null, null, 0, 0, 0, 1, 1, 1024, 1024, 10, 64, 3, 4, 0, null) == 4
     assert lib.lh_pyramid_bwd(null, null, null, 0, 0, 0, null, null, null, null, 1, 1024, 1, 128, 3, 3,
+                              0, null) == 1
+    # an element type other than LH_DTYPE_BF16 (0) / LH_DTYPE_F16 (1) is refused
+    fake = ctypes.c_void_p(64)  # never dereferenced: every call below is refused first
+    assert lib.lh_scatter_fwd(fake, fake, fake, 128, 128, 128, 1, 1, 1024, 1024, 10, 128, 3, 4, 2, null) == 1
+    assert lib.lh_scatter_bwd(fake, 128, 128, 128, fake, null, fake, null, 1, 1, 1024, 1024, 10, 128, 3, 4, 7,
                               null) == 1
+    assert lib.lh_pyramid_fwd(fake, fake, fake, 128, 128, 128, fake, fake, fake, 128, 128, 128, fake, fake,
+                              1, 1024, 1, 128, 3, 4, 0, 2, null) == 1
+    assert lib.lh_pyramid_bwd(fake, null, null, 128, 128, 128, null, fake, null, null, 1, 1024, 1, 128, 3, 4,
+                              -1, null) == 1
+    assert lib.lh_dilated_scores(fake, fake, fake, fake, fake, 1, 1024, 1, 128, 4, 1024, ctypes.c_float(0.1), 3,
+                                 null) == 1
     assert lib.lh_select_geometry(4096, 3, 4, 1536, 1, None, None, None, None) == 2
     assert lib.lh_select_geometry(4096, 1, 4, 256, 0, None, None, None, None) == 1
     # transformer-block kernels
     assert lib.lh_rope_qkv_fwd(null, 3072, null, null, null, null, 1, 16, 8, 8, 128, null) == 1
-    fake = ctypes.c_void_p(64)  # never dereferenced: every call below is refused first
     assert lib.lh_rope_pyramid_fwd(null, null, null, 0, 0, 0, null, null, null, 0, 0, 0, null, null, null,
                                    0, 0, 0, null, null, 1, 1024, 1, 128, 3, 4, null) == 1
     assert lib.lh_rope_pyramid_fwd(null, null, null, 0, 0, 0, fake, null, null, 0, 0, 0, null, null, null,
@@ -211,3 +221,17 @@ def test_row_kernels_refuse_non_bf16(pkg):
         N.attn_fwd(N.Rows(xb, xb, xb, (0, 0, 0)), idx.long(), 1, 2, 16)
     with pytest.raises(ValueError):  # head dimension not contiguous
         N.Rows(xb.transpose(-1, -2), xb, xb, (0, 0, 0))
+
+
+def test_layer_refuses_float32_and_fp16_gla(pkg):
+    """Float32 inputs are refused rather than silently downcast, and the GLA
+    scorer (bf16 kernels only) refuses fp16, all before any device work."""
+    x = torch.zeros(1, 512, 2, 128)
+    with pytest.raises(TypeError, match="bfloat16 or float16"):
+        pkg.lighthouse_layer(x, x, x, num_levels=3, pooling_factor=4, topk=128)
+    h = x.half()
+    with pytest.raises(TypeError, match="share a dtype"):
+        pkg.lighthouse_layer(h, h.bfloat16(), h, num_levels=3, pooling_factor=4, topk=128)
+    with pytest.raises(TypeError, match="GLA"):
+        pkg.lighthouse_layer(h, h, h, num_levels=3, pooling_factor=4, topk=128, dilation=4,
+                             gk=torch.zeros(1, 512, 2))
