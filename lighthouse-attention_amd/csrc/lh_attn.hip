@@ -857,7 +857,9 @@ template <typename T>
 __device__ __forceinline__ void dq_block(const AttnArgs& a, int bh, int qb, bf16_t* K0, bf16_t* K1, bf16_t* V0,
                                          bf16_t* V1, float* kc) {
   constexpr int BM = 32 * QW;
-  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  int tid = threadIdx.x;  // opaque, as in dkdv_block
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = a.n;
   const BhRows m = bh_rows(a, bh);
@@ -1222,6 +1224,227 @@ __device__ __forceinline__ void dw_mma(floatx16 (&dp)[2], floatx16 (&dka)[4], co
   mma_phase_order<8>();
 }
 
+// LDS of the key-stationary block (dkdv_block): Q and dO tiles, their lse and
+// delta, the P hand-over and the staged Q row indices.
+struct DkdvLds {
+  bf16_t *Q0, *Q1, *Q2, *Q3, *D0, *D1, *D2, *D3;
+  float *L0, *L1, *L2, *L3;
+  u32x4 (*EX)[4][64];
+  int (*IX)[BN];
+};
+
+// dK, dV of key block kblk of (b, h) bh (128 keys).  q and nblk name the
+// work queue (entries per (b, h)) that thread 0 reserves its next entry from,
+// shortly before the block ends; returns that reservation (-1: none).
+template <typename T, bool GATHER>
+__device__ __forceinline__ int dkdv_block(const AttnArgs& a, const WorkQ& q, int nblk, int bh, int kblk,
+                                          const DkdvLds& lds) {
+  bf16_t *Q0 = lds.Q0, *Q1 = lds.Q1, *Q2 = lds.Q2, *Q3 = lds.Q3;
+  bf16_t *D0 = lds.D0, *D1 = lds.D1, *D2 = lds.D2, *D3 = lds.D3;
+  float *L0 = lds.L0, *L1 = lds.L1, *L2 = lds.L2, *L3 = lds.L3;
+  u32x4(*EX)[4][64] = lds.EX;
+  int(*IX)[BN] = lds.IX;
+  // the thread index as an opaque value: values derived from it are formed here,
+  // per block, not hoisted out of a persistent block loop (they would stay live
+  // through the other blocks' code and spill)
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, pair = wave & 3;
+  const LaneLds ll = lane_lds(lane);
+  // wave-uniform by construction; said explicitly, or the compiler keeps bh * n (and the
+  // addresses derived from it) in vector registers and spills them across the loop
+  bh = __builtin_amdgcn_readfirstlane(bh);
+  kblk = __builtin_amdgcn_readfirstlane(kblk);
+  const int n = a.n;
+  const BhRows m = bh_rows(a, bh);
+  const int k0 = kblk * BMK, kw = k0 + 32 * pair, my_k = kw + l32;
+
+  u32x4 kf[8];  // K (P wave) or -V (dS wave) rows of this lane's key
+  {
+    bool pooled;
+    const uint32_t o = row_off(m, my_k, pooled) + 8 * hh;
+    const bf16_t* p = grp ? (pooled ? m.vp : m.v) + o : (pooled ? m.kp : m.k) + o;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) kf[c] = ldg16(p + 16 * c);
+    if (grp) {  // the dS waves hold -V (bf16 sign flips are exact)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) kf[c] ^= 0x80008000u;
+    }
+  }
+  const int64_t bhn = (int64_t)bh * n;
+  const bf16_t* dbase = a.dout + bhn * LH_D;
+  const float* lse_row = a.lse_in + bhn;
+  const float* dlt_row = a.delta + bhn;
+  const int jt0 = k0 / BN;  // first query tile that sees these keys
+  const int nt = (n + BN - 1) / BN;
+
+  // Copies.  The P waves copy the Q tiles (+ lse on wave 0, the Q row indices
+  // of a later tile on wave 1), the dS waves the dO tiles (+ delta on wave 4),
+  // each wave 16 rows, in their VALU phases: in step j the P waves copy tile
+  // j + 2 (phase 2j + 1) and the dS waves tile j + 3 (phase 2j + 2), each into
+  // the buffer last read in phase 2j - 1 (Q, lse) or 2j (dO, delta); every
+  // wave waits for its previous step's copies before the barrier closing its
+  // VALU phase, so tile t is in LDS from phase 2t on (Q) or 2t + 1 on (dO).
+  // Here: Q tiles jt0, jt0 + 1, dO tiles jt0 .. jt0 + 2, and the indices of
+  // Q tiles jt0 + 2, jt0 + 3.
+  if (grp == 0) {
+    int r[4];
+    rows16<GATHER>(r, m, jt0 * BN, pair, lane);
+    copy_q16(Q0, m, r, pair, lane);
+    rows16<GATHER>(r, m, (jt0 + 1) * BN, pair, lane);
+    copy_q16(Q1, m, r, pair, lane);
+    if (pair == 0) {
+      g2l4(lse_row + min(jt0 * BN + lane, n - 1), L0);
+      g2l4(lse_row + min((jt0 + 1) * BN + lane, n - 1), L1);
+    }
+    if (GATHER && pair == 1) {
+      g2l4(m.idx + min((jt0 + 2) * BN + lane, m.last), IX[2]);
+      g2l4(m.idx + min((jt0 + 3) * BN + lane, m.last), IX[3]);
+    }
+  } else {
+    copy_d16(D0, dbase, jt0 * BN, n, pair, lane);
+    copy_d16(D1, dbase, (jt0 + 1) * BN, n, pair, lane);
+    copy_d16(D2, dbase, (jt0 + 2) * BN, n, pair, lane);
+    if (pair == 0) {
+      g2l4(dlt_row + min(jt0 * BN + lane, n - 1), L0 + BN);
+      g2l4(dlt_row + min((jt0 + 1) * BN + lane, n - 1), L1 + BN);
+      g2l4(dlt_row + min((jt0 + 2) * BN + lane, n - 1), L2 + BN);
+    }
+  }
+  // the first step's dV / dK terms multiply zeros with buffer 3: make it finite
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    reinterpret_cast<u32x4*>(Q3)[tid + 512 * i] = u32x4{};
+    reinterpret_cast<u32x4*>(D3)[tid + 512 * i] = u32x4{};
+  }
+  wait_loads();  // the first tiles and the zeros are in LDS
+  block_barrier();
+
+  floatx16 acc[4];  // dV (P wave) or dK (dS wave)
+#pragma unroll
+  for (int d = 0; d < 4; ++d) acc[d] = floatx16{};
+  floatx16 sc[2] = {floatx16{}, floatx16{}};  // S - lse/(scale log2 e) (P wave) or delta - dP (dS wave)
+  u32x4 op[2][2] = {{u32x4{}, u32x4{}}, {u32x4{}, u32x4{}}};  // P or dS, bf16 operands
+  const float sl2 = a.sl2, nisl2 = -1.0f / a.sl2;
+
+  // Step j: MFMA phase (tile j, and the previous tile's accumulation), then the
+  // VALU phase with this step's copies.  The step count is rounded up to a
+  // multiple of 4 so that the buffers rotate statically; steps past the last
+  // tile copy clamped rows.  Each role runs its own loop (same barrier count)
+  // and is register-allocated on its own.
+  auto pstep = [&](int j, const bf16_t* Qc, const float* Lc, const bf16_t* Dp, bf16_t* Qn, float* Ln,
+                   const int* ixc, int* ixn) {
+    if (j <= nt) {  // steps past nt (the rounding to 4) would multiply masked tiles and add zeros
+      __builtin_amdgcn_s_setprio(1);
+      pw_mma<T>(sc, acc, kf, op, Qc, Dp, ll, Lc, nisl2);
+      __builtin_amdgcn_s_setprio(0);
+    }
+    block_barrier();
+    {  // copy Q tile j + 2 (indices staged two steps ago), its lse, and the indices of tile j + 4
+      int r[4];
+      if (GATHER)
+        rows16_lds(r, ixc, pair, lane);
+      else
+        rows16<false>(r, m, (j + 2) * BN, pair, lane);
+      copy_q16(Qn, m, r, pair, lane);
+      if (pair == 0) g2l4(lse_row + min((j + 2) * BN + lane, n - 1), Ln);
+      if (GATHER && pair == 1) g2l4(m.idx + min((j + 4) * BN + lane, m.last), ixn);
+    }
+    if (j < nt) {  // P = exp2(S sl2 - lse), masked causally and past n
+      const int q0t = j * BN;
+      const bool mask = q0t < kw + 31 || q0t + BN > n;
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        if (mask) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int q = q0t + qb * 32 + slot_key(v, hh);
+            if (my_k > q || q >= n) sc[qb][v] = -INFINITY;
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sc[qb][v] = ex2(sc[qb][v] * sl2);
+        op[qb][0] = pack_frag<T>(sc[qb], 0);
+        op[qb][1] = pack_frag<T>(sc[qb], 1);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) EX[pair][i][lane] = op[i >> 1][i & 1];
+    } else {  // past the last tile the accumulation steps add zeros
+      op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
+    }
+    // all but this step's copies have landed
+    if (pair == 0 || (GATHER && pair == 1))
+      wait_vm<5>();
+    else
+      wait_vm<4>();
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this phase's LDS writes have landed
+    block_barrier();
+  };
+  auto dstep = [&](int j, const bf16_t* Dc, const float* Lc, const bf16_t* Qp, bf16_t* Dn, float* Ln) {
+    if (j <= nt) {
+      __builtin_amdgcn_s_setprio(1);
+      dw_mma<T>(sc, acc, kf, op, Dc, Qp, ll, Lc + BN);
+      __builtin_amdgcn_s_setprio(0);
+    }
+    block_barrier();
+    copy_d16(Dn, dbase, (j + 3) * BN, n, pair, lane);  // dO tile j + 3 and its delta
+    if (pair == 0) g2l4(dlt_row + min((j + 3) * BN + lane, n - 1), Ln + BN);
+    if (j < nt) {  // dS = P (dP - delta), P from the partner P wave
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const u32x4 e0 = EX[pair][2 * qb][lane], e1 = EX[pair][2 * qb + 1][lane];
+        float pv[16];
+        unpack8_t<T>(uint4{e0.x, e0.y, e0.z, e0.w}, pv);
+        unpack8_t<T>(uint4{e1.x, e1.y, e1.z, e1.w}, pv + 8);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sc[qb][v] = pv[v] * -sc[qb][v];  // P (dP - delta)
+        op[qb][0] = pack_frag<T>(sc[qb], 0);
+        op[qb][1] = pack_frag<T>(sc[qb], 1);
+      }
+    } else {
+      op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
+    }
+    if (pair == 0)
+      wait_vm<5>();
+    else
+      wait_vm<4>();
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the partner's P was read
+    block_barrier();
+  };
+  int next = -1;  // thread 0: the reserved next entry
+  if (grp == 0) {
+    for (int j = jt0; j <= nt; j += 4) {
+      pstep(j, Q0, L0, D3, Q2, L2, IX[2], IX[0]);
+      pstep(j + 1, Q1, L1, D0, Q3, L3, IX[3], IX[1]);
+      pstep(j + 2, Q2, L2, D1, Q0, L0, IX[0], IX[2]);
+      pstep(j + 3, Q3, L3, D2, Q1, L1, IX[1], IX[3]);
+    }
+    // the dS waves' last phase is still to run: reserve the next block now
+    if (q.ctr && threadIdx.x == 0) next = wq_reserve(q, nblk, a.BH);
+    block_barrier();
+  } else {
+    block_barrier();  // the dS waves run one phase behind
+    for (int j = jt0; j <= nt; j += 4) {
+      dstep(j, D0, L0, Q3, D3, L3);
+      dstep(j + 1, D1, L1, Q0, D0, L0);
+      dstep(j + 2, D2, L2, Q1, D1, L1);
+      dstep(j + 3, D3, L3, Q2, D2, L2);
+    }
+  }
+  if (my_k < n) {
+    // the row addresses are formed here, not held through the loops (they would spill)
+    int row = my_k, half = hh;
+    asm volatile("" : "+v"(row), "+v"(half));
+    if (grp == 0)
+      store_rows<T>(a.dv + ((int64_t)bh * n + row) * LH_D, acc, 1.0f, half);
+    else
+      store_rows<T>(a.dk + ((int64_t)bh * n + row) * LH_D, acc, a.scale, half);
+  }
+  return next;
+}
+
 template <typename T, bool GATHER>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a, const WorkQ q) {
   __shared__ __attribute__((aligned(1024))) bf16_t Q0[TILE], Q1[TILE], Q2[TILE], Q3[TILE];
@@ -1230,10 +1453,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
   __shared__ u32x4 EX[4][4][64];  // P handed from each P wave to its dS wave
   __shared__ __attribute__((aligned(16))) int IX[4][BN];  // selected-row indices of the Q tiles to copy
   __shared__ int wq_s[2];
-  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = wave >> 2, pair = wave & 3;
-  const LaneLds ll = lane_lds(lane);
+  const DkdvLds lds{Q0, Q1, Q2, Q3, D0, D1, D2, D3, L0, L1, L2, L3, EX, IX};
   int bh, kblk;
   bool have = wq_first(q, a.nq, a.BH, false, bh, kblk);  // early key blocks see the most queries
   if (!have && q.ctr) have = wq_next(q, a.nq, a.BH, false, -1, 0, bh, kblk, wq_s);
@@ -1243,193 +1463,58 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
     // addresses derived from it) in vector registers and spills them across the loop
     bh = __builtin_amdgcn_readfirstlane(bh);
     kblk = __builtin_amdgcn_readfirstlane(kblk);
-    const int n = a.n;
-    const BhRows m = bh_rows(a, bh);
-    const int k0 = kblk * BMK, kw = k0 + 32 * pair, my_k = kw + l32;
-
-    u32x4 kf[8];  // K (P wave) or -V (dS wave) rows of this lane's key
-    {
-      bool pooled;
-      const uint32_t o = row_off(m, my_k, pooled) + 8 * hh;
-      const bf16_t* p = grp ? (pooled ? m.vp : m.v) + o : (pooled ? m.kp : m.k) + o;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) kf[c] = ldg16(p + 16 * c);
-      if (grp) {  // the dS waves hold -V (bf16 sign flips are exact)
-#pragma unroll
-        for (int c = 0; c < 8; ++c) kf[c] ^= 0x80008000u;
-      }
-    }
-    const int64_t bhn = (int64_t)bh * n;
-    const bf16_t* dbase = a.dout + bhn * LH_D;
-    const float* lse_row = a.lse_in + bhn;
-    const float* dlt_row = a.delta + bhn;
-    const int jt0 = k0 / BN;  // first query tile that sees these keys
-    const int nt = (n + BN - 1) / BN;
-
-    // Copies.  The P waves copy the Q tiles (+ lse on wave 0, the Q row indices
-    // of a later tile on wave 1), the dS waves the dO tiles (+ delta on wave 4),
-    // each wave 16 rows, in their VALU phases: in step j the P waves copy tile
-    // j + 2 (phase 2j + 1) and the dS waves tile j + 3 (phase 2j + 2), each into
-    // the buffer last read in phase 2j - 1 (Q, lse) or 2j (dO, delta); every
-    // wave waits for its previous step's copies before the barrier closing its
-    // VALU phase, so tile t is in LDS from phase 2t on (Q) or 2t + 1 on (dO).
-    // Here: Q tiles jt0, jt0 + 1, dO tiles jt0 .. jt0 + 2, and the indices of
-    // Q tiles jt0 + 2, jt0 + 3.
-    if (grp == 0) {
-      int r[4];
-      rows16<GATHER>(r, m, jt0 * BN, pair, lane);
-      copy_q16(Q0, m, r, pair, lane);
-      rows16<GATHER>(r, m, (jt0 + 1) * BN, pair, lane);
-      copy_q16(Q1, m, r, pair, lane);
-      if (pair == 0) {
-        g2l4(lse_row + min(jt0 * BN + lane, n - 1), L0);
-        g2l4(lse_row + min((jt0 + 1) * BN + lane, n - 1), L1);
-      }
-      if (GATHER && pair == 1) {
-        g2l4(m.idx + min((jt0 + 2) * BN + lane, m.last), IX[2]);
-        g2l4(m.idx + min((jt0 + 3) * BN + lane, m.last), IX[3]);
-      }
-    } else {
-      copy_d16(D0, dbase, jt0 * BN, n, pair, lane);
-      copy_d16(D1, dbase, (jt0 + 1) * BN, n, pair, lane);
-      copy_d16(D2, dbase, (jt0 + 2) * BN, n, pair, lane);
-      if (pair == 0) {
-        g2l4(dlt_row + min(jt0 * BN + lane, n - 1), L0 + BN);
-        g2l4(dlt_row + min((jt0 + 1) * BN + lane, n - 1), L1 + BN);
-        g2l4(dlt_row + min((jt0 + 2) * BN + lane, n - 1), L2 + BN);
-      }
-    }
-    // the first step's dV / dK terms multiply zeros with buffer 3: make it finite
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      reinterpret_cast<u32x4*>(Q3)[tid + 512 * i] = u32x4{};
-      reinterpret_cast<u32x4*>(D3)[tid + 512 * i] = u32x4{};
-    }
-    wait_loads();  // the first tiles and the zeros are in LDS
-    block_barrier();
-
-    floatx16 acc[4];  // dV (P wave) or dK (dS wave)
-#pragma unroll
-    for (int d = 0; d < 4; ++d) acc[d] = floatx16{};
-    floatx16 sc[2] = {floatx16{}, floatx16{}};  // S - lse/(scale log2 e) (P wave) or delta - dP (dS wave)
-    u32x4 op[2][2] = {{u32x4{}, u32x4{}}, {u32x4{}, u32x4{}}};  // P or dS, bf16 operands
-    const float sl2 = a.sl2, nisl2 = -1.0f / a.sl2;
-
-    // Step j: MFMA phase (tile j, and the previous tile's accumulation), then the
-    // VALU phase with this step's copies.  The step count is rounded up to a
-    // multiple of 4 so that the buffers rotate statically; steps past the last
-    // tile copy clamped rows.  Each role runs its own loop (same barrier count)
-    // and is register-allocated on its own.
-    auto pstep = [&](int j, const bf16_t* Qc, const float* Lc, const bf16_t* Dp, bf16_t* Qn, float* Ln,
-                     const int* ixc, int* ixn) {
-      if (j <= nt) {  // steps past nt (the rounding to 4) would multiply masked tiles and add zeros
-        __builtin_amdgcn_s_setprio(1);
-        pw_mma<T>(sc, acc, kf, op, Qc, Dp, ll, Lc, nisl2);
-        __builtin_amdgcn_s_setprio(0);
-      }
-      block_barrier();
-      {  // copy Q tile j + 2 (indices staged two steps ago), its lse, and the indices of tile j + 4
-        int r[4];
-        if (GATHER)
-          rows16_lds(r, ixc, pair, lane);
-        else
-          rows16<false>(r, m, (j + 2) * BN, pair, lane);
-        copy_q16(Qn, m, r, pair, lane);
-        if (pair == 0) g2l4(lse_row + min((j + 2) * BN + lane, n - 1), Ln);
-        if (GATHER && pair == 1) g2l4(m.idx + min((j + 4) * BN + lane, m.last), ixn);
-      }
-      if (j < nt) {  // P = exp2(S sl2 - lse), masked causally and past n
-        const int q0t = j * BN;
-        const bool mask = q0t < kw + 31 || q0t + BN > n;
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          if (mask) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const int q = q0t + qb * 32 + slot_key(v, hh);
-              if (my_k > q || q >= n) sc[qb][v] = -INFINITY;
-            }
-          }
-#pragma unroll
-          for (int v = 0; v < 16; ++v) sc[qb][v] = ex2(sc[qb][v] * sl2);
-          op[qb][0] = pack_frag<T>(sc[qb], 0);
-          op[qb][1] = pack_frag<T>(sc[qb], 1);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) EX[pair][i][lane] = op[i >> 1][i & 1];
-      } else {  // past the last tile the accumulation steps add zeros
-        op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
-      }
-      // all but this step's copies have landed
-      if (pair == 0 || (GATHER && pair == 1))
-        wait_vm<5>();
-      else
-        wait_vm<4>();
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this phase's LDS writes have landed
-      block_barrier();
-    };
-    auto dstep = [&](int j, const bf16_t* Dc, const float* Lc, const bf16_t* Qp, bf16_t* Dn, float* Ln) {
-      if (j <= nt) {
-        __builtin_amdgcn_s_setprio(1);
-        dw_mma<T>(sc, acc, kf, op, Dc, Qp, ll, Lc + BN);
-        __builtin_amdgcn_s_setprio(0);
-      }
-      block_barrier();
-      copy_d16(Dn, dbase, (j + 3) * BN, n, pair, lane);  // dO tile j + 3 and its delta
-      if (pair == 0) g2l4(dlt_row + min((j + 3) * BN + lane, n - 1), Ln + BN);
-      if (j < nt) {  // dS = P (dP - delta), P from the partner P wave
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          const u32x4 e0 = EX[pair][2 * qb][lane], e1 = EX[pair][2 * qb + 1][lane];
-          float pv[16];
-          unpack8_t<T>(uint4{e0.x, e0.y, e0.z, e0.w}, pv);
-          unpack8_t<T>(uint4{e1.x, e1.y, e1.z, e1.w}, pv + 8);
-#pragma unroll
-          for (int v = 0; v < 16; ++v) sc[qb][v] = pv[v] * -sc[qb][v];  // P (dP - delta)
-          op[qb][0] = pack_frag<T>(sc[qb], 0);
-          op[qb][1] = pack_frag<T>(sc[qb], 1);
-        }
-      } else {
-        op[0][0] = op[0][1] = op[1][0] = op[1][1] = u32x4{};
-      }
-      if (pair == 0)
-        wait_vm<5>();
-      else
-        wait_vm<4>();
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the partner's P was read
-      block_barrier();
-    };
-    int next = -1;  // thread 0: the reserved next entry
-    if (grp == 0) {
-      for (int j = jt0; j <= nt; j += 4) {
-        pstep(j, Q0, L0, D3, Q2, L2, IX[2], IX[0]);
-        pstep(j + 1, Q1, L1, D0, Q3, L3, IX[3], IX[1]);
-        pstep(j + 2, Q2, L2, D1, Q0, L0, IX[0], IX[2]);
-        pstep(j + 3, Q3, L3, D2, Q1, L1, IX[1], IX[3]);
-      }
-      // the dS waves' last phase is still to run: reserve the next block now
-      if (q.ctr && threadIdx.x == 0) next = wq_reserve(q, a.nq, a.BH);
-      block_barrier();
-    } else {
-      block_barrier();  // the dS waves run one phase behind
-      for (int j = jt0; j <= nt; j += 4) {
-        dstep(j, D0, L0, Q3, D3, L3);
-        dstep(j + 1, D1, L1, Q0, D0, L0);
-        dstep(j + 2, D2, L2, Q1, D1, L1);
-        dstep(j + 3, D3, L3, Q2, D2, L2);
-      }
-    }
-    if (my_k < n) {
-      // the row addresses are formed here, not held through the loops (they would spill)
-      int row = my_k, half = hh;
-      asm volatile("" : "+v"(row), "+v"(half));
-      if (grp == 0)
-        store_rows<T>(a.dv + ((int64_t)bh * n + row) * LH_D, acc, 1.0f, half);
-      else
-        store_rows<T>(a.dk + ((int64_t)bh * n + row) * LH_D, acc, a.scale, half);
-    }
+    const int next = dkdv_block<T, GATHER>(a, q, a.nq, bh, kblk, lds);
     if (!q.ctr) break;
     have = wq_next(q, a.nq, a.BH, false, next, ++nrun, bh, kblk, wq_s);  // the previous block's copies are waited for there
+  }
+}
+
+// ===========================================================================
+// backward in one persistent launch (dK/dV and dQ blocks from shared queues)
+//
+// The dK/dV and dQ kernels each end in a tail where their last blocks leave
+// CUs idle (about 28 us per launch at cfg2, from per-workgroup timestamps), and
+// the dQ plan cannot follow the XCDs' different speeds (its slowest XCD ends
+// 40 us after the fastest).  Run together, the two kinds of block share one
+// set of per-XCD work queues: each (b, h) contributes its dK/dV key blocks and
+// its dQ query blocks, in one order, heaviest first by their MFMA work, so the
+// lightest blocks of both kinds fill the end of the launch.  Each block is
+// computed whole by one workgroup, by the same code as in the separate
+// kernels, so the results are bit-equal to theirs.  The dQ block's K/V tiles
+// and key centre alias the dK/dV block's Q and dO buffers: a workgroup runs
+// one block at a time, with its loads waited for and a barrier in between.
+// ===========================================================================
+constexpr int BWD_ORDER_MAX = 1024;
+constexpr uint16_t BWD_DQ = 0x8000;  // item bit: a dQ query block (else a dK/dV key block)
+struct BwdOrder {
+  int n;  // items per (b, h)
+  uint16_t item[BWD_ORDER_MAX];
+};
+
+template <typename T, bool GATHER>
+__global__ __launch_bounds__(512, 1) void attn_bwd_kernel(const AttnArgs a, const WorkQ q, const BwdOrder ord) {
+  __shared__ __attribute__((aligned(1024))) bf16_t Q0[TILE], Q1[TILE], Q2[TILE], Q3[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t D0[TILE], D1[TILE], D2[TILE], D3[TILE];
+  __shared__ __attribute__((aligned(16))) float L0[2 * BN], L1[2 * BN], L2[2 * BN], L3[2 * BN];
+  __shared__ u32x4 EX[4][4][64];
+  __shared__ __attribute__((aligned(16))) int IX[4][BN];
+  __shared__ int wq_s[2];
+  static_assert((128 + QW * 132) * sizeof(float) <= TILE * sizeof(bf16_t), "the key centre fits one tile buffer");
+  const DkdvLds lds{Q0, Q1, Q2, Q3, D0, D1, D2, D3, L0, L1, L2, L3, EX, IX};
+  int bh, r;
+  bool have = wq_first(q, ord.n, a.BH, false, bh, r);
+  if (!have) have = wq_next(q, ord.n, a.BH, false, -1, 0, bh, r, wq_s);
+  int nrun = 0;
+  while (have) {
+    bh = __builtin_amdgcn_readfirstlane(bh);
+    r = __builtin_amdgcn_readfirstlane(r);
+    const int e = ord.item[r];
+    int next = -1;
+    if (e & BWD_DQ)
+      dq_block<T>(a, bh, e & ~BWD_DQ, Q0, Q1, Q2, Q3, reinterpret_cast<float*>(D0));
+    else
+      next = dkdv_block<T, GATHER>(a, q, ord.n, bh, e, lds);
+    have = wq_next(q, ord.n, a.BH, false, next, ++nrun, bh, r, wq_s);
   }
 }
 
@@ -2013,6 +2098,40 @@ extern "C" int lh_attn_fwd(const void* q, const void* k, const void* v, int64_t 
 }
 
 namespace {
+// Item order of the fused backward for length n: every dK/dV key block (128
+// keys: about 256 MFMAs per CU for each of its ceil(n / 64) - 2 kblk query
+// tiles) and dQ query block (256 queries: 384 MFMAs per key tile, 4 (qb + 1)
+// tiles, at the 4% higher rate the dQ kernel reaches), plus about 1.5 tiles
+// of set-up and stores each, sorted heaviest first (ties: dK/dV first, lower
+// block first).  Cached per n; false when there are more items than fit.
+bool bwd_order(int n, BwdOrder& o) {
+  static std::mutex mu;
+  static std::map<int, BwdOrder> cache;
+  {
+    std::lock_guard<std::mutex> g(mu);
+    auto it = cache.find(n);
+    if (it != cache.end()) {
+      o = it->second;
+      return o.n > 0;
+    }
+  }
+  const int nt = (n + BN - 1) / BN, nkb = (n + BMK - 1) / BMK, nqb = (n + 32 * QW - 1) / (32 * QW);
+  o.n = 0;
+  if (nkb + nqb <= BWD_ORDER_MAX) {
+    std::vector<std::pair<double, int>> w;
+    for (int kb = 0; kb < nkb; ++kb) w.push_back({256.0 * (std::max(nt - 2 * kb, 1) + 1.5), kb});
+    for (int qb = 0; qb < nqb; ++qb) w.push_back({384.0 / 1.04 * (std::min(4 * (qb + 1), nt) + 1.5), BWD_DQ | qb});
+    std::stable_sort(w.begin(), w.end(), [](const std::pair<double, int>& x, const std::pair<double, int>& y) {
+      return x.first > y.first;
+    });
+    for (const auto& e : w) o.item[o.n++] = (uint16_t)e.second;
+  }
+  std::lock_guard<std::mutex> g(mu);
+  if (cache.size() >= 256) cache.clear();
+  cache[n] = o;
+  return o.n > 0;
+}
+
 // parts: bit 0 = dK/dV kernel, bit 1 = dQ kernel
 int attn_bwd_parts(int parts, const void* q, const void* k, const void* v, int64_t sb, int64_t ss, int64_t sh,
                    const void* qp, const void* kp, const void* vp, int64_t pb, int64_t ps, int64_t ph, int split,
@@ -2028,6 +2147,24 @@ int attn_bwd_parts(int parts, const void* q, const void* k, const void* v, int64
   a.dout = (const bf16_t*)dout; a.lse_in = lse; a.delta = delta;
   a.dq = (bf16_t*)dq; a.dk = (bf16_t*)dk; a.dv = (bf16_t*)dv;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // Both halves: one persistent launch where work queues apply (bf16; for fp16
+  // rows the fused kernel's uniform state does not fit the scalar registers
+  // without spilling, so fp16 runs the two kernels one after the other).
+  if (parts == 3 && dtype == LH_DTYPE_BF16) {
+    BwdOrder ord;
+    WorkQ wq;
+    if (bwd_order(a.n, ord)) {
+      const int grid = wq_grid(ord.n, a.BH, st, wq);
+      if (wq.ctr) {
+        if (indices)
+          hipLaunchKernelGGL((attn_bwd_kernel<BF16, true>), dim3(grid), dim3(512), 0, st, a, wq, ord);
+        else
+          hipLaunchKernelGGL((attn_bwd_kernel<BF16, false>), dim3(grid), dim3(512), 0, st, a, wq, ord);
+        LH_CHECK_LAUNCH();
+        return LH_OK;
+      }
+    }
+  }
   if (parts & 1) {
     AttnArgs ak = a;
     ak.nq = (a.n + BMK - 1) / BMK;

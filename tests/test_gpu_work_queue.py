@@ -298,3 +298,34 @@ def test_queue_two_graphs_on_two_streams(pkg, dev):
                 assert torch.equal(x, y), f"replay {r}, graph {i}: {name} differs from the eager result"
         assert torch.equal(eager[0], ref[0])
     assert N.attn_status(dev) == 0
+
+
+@pytest.mark.parametrize("n,B,H,gathered", [(18432, 1, 8, True), (30000, 1, 3, False), (5000, 2, 4, True)])
+def test_fused_backward_bit_equal(pkg, dev, n, B, H, gathered):
+    """lh_attn_bwd runs dK/dV and dQ blocks in one persistent launch (shared work
+    queues) where queues apply: bit-equal to the two separate kernels, over
+    repeated launches."""
+    print(f"fused backward n={n} B={B} H={H} gathered={gathered}", flush=True)
+    N = pkg._native
+    S, Sp = n, n // 3
+    xs = [_rand((B, S, H, 128), 130 + i, dev) for i in range(3)]
+    if gathered:
+        pxs = [_rand((B, Sp, H, 128), 140 + i, dev) for i in range(3)]
+        g = torch.Generator().manual_seed(n)
+        idx = torch.stack([torch.stack([torch.randperm(S + Sp, generator=g)[:n] for _ in range(H)])
+                           for _ in range(B)]).int().to(dev)
+        rows = N.Rows(*xs, (xs[0].stride(0), xs[0].stride(1), xs[0].stride(2)), *pxs,
+                      (pxs[0].stride(0), pxs[0].stride(1), pxs[0].stride(2)), split=S)
+    else:
+        idx = None
+        rows = N.Rows(*xs, (xs[0].stride(0), xs[0].stride(1), xs[0].stride(2)))
+    o, lse = N.attn_fwd(rows, idx, B, H, n)
+    do = _rand((B, H, n, 128), 150, dev)
+    delta = (do.float() * o.float()).sum(-1)
+    dk, dv = N.attn_bwd_dkdv(rows, idx, B, H, n, do, lse, delta)
+    dq = N.attn_bwd_dq(rows, idx, B, H, n, do, lse, delta)
+    for r in range(3):
+        got = N.attn_bwd(rows, idx, B, H, n, do, lse, delta)
+        for name, x, y in zip(("dq", "dk", "dv"), got, (dq, dk, dv)):
+            assert torch.equal(x, y), f"launch {r}: fused {name} differs from the separate kernel"
+    assert N.attn_status(dev) == 0
