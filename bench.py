@@ -116,7 +116,6 @@ def algorithmic_work(w, S_sel):
         "scatter_bwd": ("bytes", ((S_sel + S) * H * D * e + S_sel * H * D * e + S_sel * H * 4 * 2) * B),
         "attn_bwd_dkdv": ("flop", 8 * D * pairs),       # S, dP, dV, dK passes
         "attn_bwd_dq": ("flop", 2 * D * pairs),         # the dQ pass (S and dP are recomputed)
-        "attn_bwd": ("flop", 10 * D * pairs),           # both in one launch: S, dP, dV, dK and dQ
         "pyramid_bwd": ("bytes", (3 * S_sel * H * D * e + 3 * S * H * D * e + S_tot * H * 4) * B),
     }
     if w["scorer"] == "dilated":
@@ -196,18 +195,15 @@ def run_gpu(args, pkg, torch):
         cfg["dilation"] = w["dilation"]
     if w.get("heavy_keys"):
         cfg["heavy_keys"] = w["heavy_keys"]
-    # the attention backward (dK/dV + dQ) against its algorithmic work, 2.5x the
-    # forward's (S, dP, dV, dK and dQ products; the dQ blocks' recomputed S and dP are
-    # not counted): one launch by default; with the two-stream schedule the kernels
-    # overlap, and the pair's time is the longer of the two
+    # the backward pair (dK/dV + dQ kernels) against the attention backward's algorithmic
+    # work, 2.5x the forward's (S, dP, dV, dK and dQ products; the dQ kernel's recomputed
+    # S and dP are not counted); with the two-stream schedule the kernels overlap, and
+    # the pair's time is the longer of the two
+    kd, kq = kernels["attn_bwd_dkdv"], kernels["attn_bwd_dq"]
     two = sel_mod._bwd_streams >= 2
-    if "attn_bwd" in kernels:
-        pair_ms, pair_work, sched = kernels["attn_bwd"]["ms"], kernels["attn_bwd"]["work"], "one launch"
-    else:
-        kd, kq = kernels["attn_bwd_dkdv"], kernels["attn_bwd_dq"]
-        pair_ms = max(kd["ms"], kq["ms"]) if two else kd["ms"] + kq["ms"]
-        pair_work = kd["work"] + kq["work"]
-        sched = "two streams" if two else "one stream, dK/dV then dQ"
+    pair_ms = max(kd["ms"], kq["ms"]) if two else kd["ms"] + kq["ms"]
+    pair_work = kd["work"] + kq["work"]
+    sched = "two streams" if two else "one stream, dK/dV then dQ"
     pair = {"ms": round(pair_ms, 4), "algorithmic_tflop": round(pair_work / 1e12, 4),
             "achieved": round(pair_work / (pair_ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
             "frac": round(pair_work / (pair_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),

@@ -1470,55 +1470,6 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
 }
 
 // ===========================================================================
-// backward in one persistent launch (dK/dV and dQ blocks from shared queues)
-//
-// The dK/dV and dQ kernels each end in a tail where their last blocks leave
-// CUs idle (about 28 us per launch at cfg2, from per-workgroup timestamps), and
-// the dQ plan cannot follow the XCDs' different speeds (its slowest XCD ends
-// 40 us after the fastest).  Run together, the two kinds of block share one
-// set of per-XCD work queues: each (b, h) contributes its dK/dV key blocks and
-// its dQ query blocks, in one order, heaviest first by their MFMA work, so the
-// lightest blocks of both kinds fill the end of the launch.  Each block is
-// computed whole by one workgroup, by the same code as in the separate
-// kernels, so the results are bit-equal to theirs.  The dQ block's K/V tiles
-// and key centre alias the dK/dV block's Q and dO buffers: a workgroup runs
-// one block at a time, with its loads waited for and a barrier in between.
-// ===========================================================================
-constexpr int BWD_ORDER_MAX = 1024;
-constexpr uint16_t BWD_DQ = 0x8000;  // item bit: a dQ query block (else a dK/dV key block)
-struct BwdOrder {
-  int n;  // items per (b, h)
-  uint16_t item[BWD_ORDER_MAX];
-};
-
-template <typename T, bool GATHER>
-__global__ __launch_bounds__(512, 1) void attn_bwd_kernel(const AttnArgs a, const WorkQ q, const BwdOrder ord) {
-  __shared__ __attribute__((aligned(1024))) bf16_t Q0[TILE], Q1[TILE], Q2[TILE], Q3[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t D0[TILE], D1[TILE], D2[TILE], D3[TILE];
-  __shared__ __attribute__((aligned(16))) float L0[2 * BN], L1[2 * BN], L2[2 * BN], L3[2 * BN];
-  __shared__ u32x4 EX[4][4][64];
-  __shared__ __attribute__((aligned(16))) int IX[4][BN];
-  __shared__ int wq_s[2];
-  static_assert((128 + QW * 132) * sizeof(float) <= TILE * sizeof(bf16_t), "the key centre fits one tile buffer");
-  const DkdvLds lds{Q0, Q1, Q2, Q3, D0, D1, D2, D3, L0, L1, L2, L3, EX, IX};
-  int bh, r;
-  bool have = wq_first(q, ord.n, a.BH, false, bh, r);
-  if (!have) have = wq_next(q, ord.n, a.BH, false, -1, 0, bh, r, wq_s);
-  int nrun = 0;
-  while (have) {
-    bh = __builtin_amdgcn_readfirstlane(bh);
-    r = __builtin_amdgcn_readfirstlane(r);
-    const int e = ord.item[r];
-    int next = -1;
-    if (e & BWD_DQ)
-      dq_block<T>(a, bh, e & ~BWD_DQ, Q0, Q1, Q2, Q3, reinterpret_cast<float*>(D0));
-    else
-      next = dkdv_block<T, GATHER>(a, q, ord.n, bh, e, lds);
-    have = wq_next(q, ord.n, a.BH, false, next, ++nrun, bh, r, wq_s);
-  }
-}
-
-// ===========================================================================
 // GLA scorer: simple gated linear attention over the dilated virtual heads,
 //   o_t = scale * sum_{s <= t} exp(G_t - G_s) (q_t . k_s) v_s,  G = cumsum(g),
 // and the bf16-rounded L2 norm of the bf16-rounded o_t as the base score.
@@ -2098,40 +2049,6 @@ extern "C" int lh_attn_fwd(const void* q, const void* k, const void* v, int64_t 
 }
 
 namespace {
-// Item order of the fused backward for length n: every dK/dV key block (128
-// keys: about 256 MFMAs per CU for each of its ceil(n / 64) - 2 kblk query
-// tiles) and dQ query block (256 queries: 384 MFMAs per key tile, 4 (qb + 1)
-// tiles, at the 4% higher rate the dQ kernel reaches), plus about 1.5 tiles
-// of set-up and stores each, sorted heaviest first (ties: dK/dV first, lower
-// block first).  Cached per n; false when there are more items than fit.
-bool bwd_order(int n, BwdOrder& o) {
-  static std::mutex mu;
-  static std::map<int, BwdOrder> cache;
-  {
-    std::lock_guard<std::mutex> g(mu);
-    auto it = cache.find(n);
-    if (it != cache.end()) {
-      o = it->second;
-      return o.n > 0;
-    }
-  }
-  const int nt = (n + BN - 1) / BN, nkb = (n + BMK - 1) / BMK, nqb = (n + 32 * QW - 1) / (32 * QW);
-  o.n = 0;
-  if (nkb + nqb <= BWD_ORDER_MAX) {
-    std::vector<std::pair<double, int>> w;
-    for (int kb = 0; kb < nkb; ++kb) w.push_back({256.0 * (std::max(nt - 2 * kb, 1) + 1.5), kb});
-    for (int qb = 0; qb < nqb; ++qb) w.push_back({384.0 / 1.04 * (std::min(4 * (qb + 1), nt) + 1.5), BWD_DQ | qb});
-    std::stable_sort(w.begin(), w.end(), [](const std::pair<double, int>& x, const std::pair<double, int>& y) {
-      return x.first > y.first;
-    });
-    for (const auto& e : w) o.item[o.n++] = (uint16_t)e.second;
-  }
-  std::lock_guard<std::mutex> g(mu);
-  if (cache.size() >= 256) cache.clear();
-  cache[n] = o;
-  return o.n > 0;
-}
-
 // parts: bit 0 = dK/dV kernel, bit 1 = dQ kernel
 int attn_bwd_parts(int parts, const void* q, const void* k, const void* v, int64_t sb, int64_t ss, int64_t sh,
                    const void* qp, const void* kp, const void* vp, int64_t pb, int64_t ps, int64_t ph, int split,
@@ -2147,24 +2064,6 @@ int attn_bwd_parts(int parts, const void* q, const void* k, const void* v, int64
   a.dout = (const bf16_t*)dout; a.lse_in = lse; a.delta = delta;
   a.dq = (bf16_t*)dq; a.dk = (bf16_t*)dk; a.dv = (bf16_t*)dv;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  // Both halves: one persistent launch where work queues apply (bf16; for fp16
-  // rows the fused kernel's uniform state does not fit the scalar registers
-  // without spilling, so fp16 runs the two kernels one after the other).
-  if (parts == 3 && dtype == LH_DTYPE_BF16) {
-    BwdOrder ord;
-    WorkQ wq;
-    if (bwd_order(a.n, ord)) {
-      const int grid = wq_grid(ord.n, a.BH, st, wq);
-      if (wq.ctr) {
-        if (indices)
-          hipLaunchKernelGGL((attn_bwd_kernel<BF16, true>), dim3(grid), dim3(512), 0, st, a, wq, ord);
-        else
-          hipLaunchKernelGGL((attn_bwd_kernel<BF16, false>), dim3(grid), dim3(512), 0, st, a, wq, ord);
-        LH_CHECK_LAUNCH();
-        return LH_OK;
-      }
-    }
-  }
   if (parts & 1) {
     AttnArgs ak = a;
     ak.nq = (a.n + BMK - 1) / BMK;

@@ -106,10 +106,9 @@ _op_hook = None
 def set_op_hook(fn):
     """Install ``fn(name)``, called on the host right after each native op of the
     layer is enqueued (names: ``pyramid``, ``dilated_scores``, ``select``,
-    ``attn_fwd``, ``scatter_fwd``, ``scatter_bwd``, ``attn_bwd`` (or, with two
-    backward streams, ``attn_bwd_dkdv`` and ``attn_bwd_dq``), ``pyramid_bwd``)
-    and with ``fwd_start`` / ``bwd_start`` before the first one; e.g. to record a
-    stream event per op.  The dense causal
+    ``attn_fwd``, ``scatter_fwd``, ``scatter_bwd``, ``attn_bwd_dkdv``,
+    ``attn_bwd_dq``, ``pyramid_bwd``) and with ``fwd_start`` / ``bwd_start``
+    before the first one; e.g. to record a stream event per op.  The dense causal
     layers report ``dense_attn_fwd`` / ``dense_attn_bwd`` after ``dense_fwd_start`` /
     ``dense_bwd_start``.  ``None`` removes it."""
     global _op_hook
@@ -153,18 +152,17 @@ def _layer_fwd(xq, xk, xv, L, p, topk, tie, strict, dilation, seq_major, gk=None
     return out, idx, (pq, pk, pv, inv, o, lse)
 
 
-# The dK/dV and dQ halves are independent.  One stream is the default: both run in
-# one persistent launch (lh_attn_bwd) that takes their blocks from shared work
-# queues where those apply, else one after the other.  With two streams the dQ
-# kernel runs on a side stream (default priority) beside the dK/dV kernel; its
-# query-block plan assumes the whole GPU, and that measured slower.
+# The dK/dV and dQ kernels are independent: with two streams the dQ kernel runs on a
+# side stream (default priority) beside the dK/dV kernel.  One stream is the default:
+# the dQ kernel's query-block plan assumes the whole GPU, and beside the dK/dV kernel
+# the pair measured slower than one after the other.
 _bwd_streams = int(os.environ.get("LH_BWD_STREAMS", "1"))
 _side = {}
 
 
 def set_backward_streams(n: int) -> int:
-    """1: the attention backward on the caller's stream (one launch where work
-    queues apply); 2: dQ on a side stream beside dK/dV.  Returns the previous setting."""
+    """1: dK/dV then dQ on the caller's stream; 2: dQ on a side stream beside dK/dV.
+    Returns the previous setting."""
     global _bwd_streams
     prev, _bwd_streams = _bwd_streams, int(n)
     return prev
@@ -172,8 +170,10 @@ def set_backward_streams(n: int) -> int:
 
 def _attn_bwd_pair(rows, idx, B, H, S_sel, dattn, lse, delta, D, scale=None):
     if _bwd_streams < 2 or torch.compiler.is_compiling():
-        dqs, dks, dvs = N.attn_bwd(rows, idx, B, H, S_sel, dattn, lse, delta, D, scale)
-        _mark("attn_bwd")
+        dks, dvs = N.attn_bwd_dkdv(rows, idx, B, H, S_sel, dattn, lse, delta, D, scale)
+        _mark("attn_bwd_dkdv")
+        dqs = N.attn_bwd_dq(rows, idx, B, H, S_sel, dattn, lse, delta, D, scale)
+        _mark("attn_bwd_dq")
         return dqs, dks, dvs
     dev = dattn.device
     main = torch.cuda.current_stream(dev)

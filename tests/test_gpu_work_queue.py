@@ -301,11 +301,10 @@ def test_queue_two_graphs_on_two_streams(pkg, dev):
 
 
 @pytest.mark.parametrize("n,B,H,gathered", [(18432, 1, 8, True), (30000, 1, 3, False), (5000, 2, 4, True)])
-def test_fused_backward_bit_equal(pkg, dev, n, B, H, gathered):
-    """lh_attn_bwd runs dK/dV and dQ blocks in one persistent launch (shared work
-    queues) where queues apply: bit-equal to the two separate kernels, over
-    repeated launches."""
-    print(f"fused backward n={n} B={B} H={H} gathered={gathered}", flush=True)
+def test_backward_halves_bit_equal(pkg, dev, n, B, H, gathered):
+    """lh_attn_bwd equals its two halves (lh_attn_bwd_dkdv, lh_attn_bwd_dq) bit
+    for bit, over repeated launches on one stream's counter slot."""
+    print(f"backward halves n={n} B={B} H={H} gathered={gathered}", flush=True)
     N = pkg._native
     S, Sp = n, n // 3
     xs = [_rand((B, S, H, 128), 130 + i, dev) for i in range(3)]
@@ -327,5 +326,5 @@ def test_fused_backward_bit_equal(pkg, dev, n, B, H, gathered):
     for r in range(3):
         got = N.attn_bwd(rows, idx, B, H, n, do, lse, delta)
         for name, x, y in zip(("dq", "dk", "dv"), got, (dq, dk, dv)):
-            assert torch.equal(x, y), f"launch {r}: fused {name} differs from the separate kernel"
+            assert torch.equal(x, y), f"launch {r}: {name} differs from the separate kernel's"
     assert N.attn_status(dev) == 0
