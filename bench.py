@@ -408,6 +408,9 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB five times (reference kernel of known "
                          "traffic for the FETCH_SIZE / WRITE_SIZE counters) and exit")
+    ap.add_argument("--schedule", default="auto", choices=["auto", "noplan", "noqueue", "plain"],
+                    help="attention launch scheduling, for A/B runs: auto (plans and work queues where the "
+                         "shape calls for them), noplan, noqueue, or plain (one block per workgroup)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU per process and has no multi-GPU path; "
@@ -425,6 +428,9 @@ def main():
         return
     import __graft_entry__ as G
     pkg = G.load_package()
+    if args.schedule != "auto":
+        pkg._native.set_attention_schedule(plans=args.schedule not in ("noplan", "plain"),
+                                           queues=args.schedule not in ("noqueue", "plain"))
     model = args.workload in MODEL_WORKLOADS
     r = run_model(args, pkg, torch) if model else run_gpu(args, pkg, torch)
     # the CPU oracle covers the layer; a CPU training step of the 270M model is not sampled
@@ -451,6 +457,8 @@ def main():
         "kernels": r["kernels"],
         "wall_ms_per_step": round(r["wall_ms_step"], 4),
     }
+    if args.schedule != "auto":
+        line["config"]["schedule"] = args.schedule
     for key in ("backward_pair", "native_ms_per_step", "final_loss"):
         if key in r:
             line[key] = r[key]

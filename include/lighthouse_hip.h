@@ -40,7 +40,7 @@ extern "C" {
 #define LH_ERR_RUNTIME 5      /* a HIP runtime call (synchronize, copy, symbol lookup) failed */
 
 /* The ABI this header declares; lh_abi_version() of a matching library returns it. */
-#define LH_ABI_VERSION 7
+#define LH_ABI_VERSION 8
 
 #define LH_DTYPE_BF16 0       /* row element type: bfloat16 (the reference configs) */
 #define LH_DTYPE_F16 1        /* row element type: IEEE half */
@@ -284,6 +284,22 @@ int lh_attn_status(int *faults);
  * dirty slot.  No counterpart in the reference.
  */
 int lh_attn_queue_slot(void *stream, void **slot);
+
+/*
+ * Scheduling of the attention launches (lh_attn_fwd, lh_attn_bwd*,
+ * lh_dilated_scores) in this process, for A/B measurement: 0 (the default)
+ * lets each launch choose a packed query-block plan, per-XCD work queues or one
+ * block per workgroup by its shape; LH_SCHED_NO_PLAN never uses a plan,
+ * LH_SCHED_NO_QUEUE never uses the queues; both together give one block per
+ * workgroup everywhere.  Outputs are bit-identical under every setting (each
+ * block's arithmetic is the same).  *previous (if not NULL) receives the old
+ * flags; unknown bits give LH_ERR_INVALID_ARG.  Takes effect for launches issued
+ * after the call; a graph keeps the schedule it was captured with.  No
+ * counterpart in the reference.
+ */
+#define LH_SCHED_NO_PLAN 1
+#define LH_SCHED_NO_QUEUE 2
+int lh_attn_set_schedule(int flags, int *previous);
 
 /*
  * Fan-out of each selected row onto the base positions it stands for:

@@ -54,6 +54,7 @@ _SIGS = {
                             _I, _I, _I, _I, _F, _P, _P, _P, _P, _I, _P]),
     "lh_attn_status": (_I, [_P]),
     "lh_attn_queue_slot": (_I, [_P, _P]),
+    "lh_attn_set_schedule": (_I, [_I, _P]),
     "lh_scatter_fwd": (_I, [_P, _P, _P, _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_scatter_bwd": (_I, [_P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_pyramid_bwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
@@ -387,6 +388,21 @@ def attn_status(device=None) -> int:
         rc = lib().lh_attn_status(ctypes.byref(f))
     _check(rc, "lh_attn_status")
     return f.value
+
+
+SCHED_NO_PLAN = 1   # LH_SCHED_NO_PLAN
+SCHED_NO_QUEUE = 2  # LH_SCHED_NO_QUEUE
+
+
+def set_attention_schedule(plans: bool = True, queues: bool = True):
+    """Let the attention launches of this process use packed query-block plans
+    and per-XCD work queues where their shape calls for them (the default), or
+    keep them from it, for A/B measurement; outputs are bit-identical either
+    way.  Returns the previous setting as ``(plans, queues)``."""
+    prev = ctypes.c_int(0)
+    flags = (0 if plans else SCHED_NO_PLAN) | (0 if queues else SCHED_NO_QUEUE)
+    _check(lib().lh_attn_set_schedule(flags, ctypes.byref(prev)), "lh_attn_set_schedule")
+    return (not prev.value & SCHED_NO_PLAN, not prev.value & SCHED_NO_QUEUE)
 
 
 def _check_queues(dev, what: str):

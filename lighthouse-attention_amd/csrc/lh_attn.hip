@@ -1885,11 +1885,14 @@ bool pack_bfd(const std::vector<int>& w, const std::vector<int>& order, int nb, 
 // heaviest block and the mean) for which they fit.  No plan (one block per
 // workgroup) when the bins would not fill whole XCDs or every block has a CU
 // of its own anyway.  Plans are cached per geometry.  Returns the grid size.
+std::atomic<int> g_schedule{0};  // LH_SCHED_* flags (lh_attn_set_schedule)
+
 int make_plan(int BH, int n, QPlan& p) {
   p.bph = 0;
   p.ipb = 0;
   const int nb = (n + 32 * QW - 1) / (32 * QW);
   const int plain = nb * BH;
+  if (g_schedule.load(std::memory_order_relaxed) & LH_SCHED_NO_PLAN) return plain;
   const int cus = cu_count();
   if (cus <= 0 || cus % 8 || BH % 8 || BH > cus || (cus / 8) % (BH / 8)) return plain;
   const int bph = cus / BH;
@@ -2013,6 +2016,7 @@ int wq_grid(int nblk, int BH, hipStream_t st, WorkQ& q) {
   const long long total = (long long)nblk * BH;
   const int cus = cu_count();
   if (cus <= 0 || cus % 8 || total <= cus || total > 12LL * cus) return (int)total;
+  if (g_schedule.load(std::memory_order_relaxed) & LH_SCHED_NO_QUEUE) return (int)total;
   unsigned* c = wq_counters(st);
   if (!c) return (int)total;
   q.ctr = c;
@@ -2144,6 +2148,13 @@ extern "C" int lh_attn_status(int* faults) {
     if (!n) n = 1;
   }
   *faults = n;
+  return LH_OK;
+}
+
+extern "C" int lh_attn_set_schedule(int flags, int* previous) {
+  if (flags & ~(LH_SCHED_NO_PLAN | LH_SCHED_NO_QUEUE)) return LH_ERR_INVALID_ARG;
+  const int old = g_schedule.exchange(flags);
+  if (previous) *previous = old;
   return LH_OK;
 }
 

@@ -48,6 +48,20 @@ def test_abi_version_matches_header(pkg):
     assert pkg._native.lib().lh_abi_version() == int(m.group(1))
 
 
+def test_attention_schedule_switch(pkg):
+    """Host-only: the schedule flags round-trip, unknown bits are refused and
+    leave the setting alone, and the default is restored."""
+    lib = pkg._native.lib()
+    prev = ctypes.c_int(-1)
+    assert lib.lh_attn_set_schedule(3, ctypes.byref(prev)) == 0
+    assert prev.value == 0
+    assert lib.lh_attn_set_schedule(4, ctypes.byref(prev)) == 1  # LH_ERR_INVALID_ARG
+    assert lib.lh_attn_set_schedule(1, ctypes.byref(prev)) == 0
+    assert prev.value == 3
+    assert pkg._native.set_attention_schedule() == (False, True)
+    assert pkg._native.set_attention_schedule() == (True, True)
+
+
 def test_gla_workspace_geometry(pkg):
     """Host-only size query of the segmented GLA walk: one segment needs no
     workspace; otherwise (P - 1) fp32 128 x 128 states plus one decay per

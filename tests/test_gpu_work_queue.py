@@ -328,3 +328,38 @@ def test_backward_halves_bit_equal(pkg, dev, n, B, H, gathered):
         for name, x, y in zip(("dq", "dk", "dv"), got, (dq, dk, dv)):
             assert torch.equal(x, y), f"launch {r}: {name} differs from the separate kernel's"
     assert N.attn_status(dev) == 0
+
+
+@pytest.mark.parametrize("n,B,H", [(18432, 1, 8), (18432, 1, 4)])
+def test_schedule_switch_bit_equal(pkg, dev, n, B, H):
+    """lh_attn_set_schedule: the forward and backward with plans and queues
+    off, each off alone and the default all give the same bits (cfg2's shape
+    uses plans for the forward and dQ and queues for dK/dV; 4 heads use queues
+    for all three)."""
+    print(f"schedule switch n={n} B={B} H={H}", flush=True)
+    N = pkg._native
+    S, Sp = n, n // 3
+    xs = [_rand((B, S, H, 128), 160 + i, dev) for i in range(3)]
+    pxs = [_rand((B, Sp, H, 128), 170 + i, dev) for i in range(3)]
+    g = torch.Generator().manual_seed(n + H)
+    idx = torch.stack([torch.stack([torch.randperm(S + Sp, generator=g)[:n] for _ in range(H)])
+                       for _ in range(B)]).int().to(dev)
+    rows = N.Rows(*xs, (xs[0].stride(0), xs[0].stride(1), xs[0].stride(2)), *pxs,
+                  (pxs[0].stride(0), pxs[0].stride(1), pxs[0].stride(2)), split=S)
+    do = _rand((B, H, n, 128), 180, dev)
+
+    def run():
+        o, lse = N.attn_fwd(rows, idx, B, H, n)
+        delta = (do.float() * o.float()).sum(-1)
+        return (o, lse) + tuple(N.attn_bwd(rows, idx, B, H, n, do, lse, delta))
+
+    ref = run()
+    try:
+        for plans, queues in ((False, False), (False, True), (True, False), (True, True)):
+            N.set_attention_schedule(plans=plans, queues=queues)
+            got = run()
+            for name, x, y in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
+                assert torch.equal(x, y), f"plans={plans} queues={queues}: {name} differs from the default"
+    finally:
+        N.set_attention_schedule()
+    assert N.attn_status(dev) == 0
