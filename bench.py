@@ -1,6 +1,6 @@
 """Lighthouse layer forward+backward throughput on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload cfg2] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 200] [--workload cfg2] [--no-cpu-baseline]
 
 A step is one forward + backward of one Lighthouse layer over one batch of
 seeded synthetic N(0,1) bf16 tensors already resident in HBM: pyramid + scores
@@ -399,7 +399,10 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps before the timed ones (default: 200 for the layer workloads, about "
+                         "0.6 s at cfg2, since the GPU clock settles over the first fraction of a second of "
+                         "load and the timed steps should see it settled; 5 for the model step)")
     ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS) + sorted(MODEL_WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=0,
@@ -432,6 +435,8 @@ def main():
         pkg._native.set_attention_schedule(plans=args.schedule not in ("noplan", "plain"),
                                            queues=args.schedule not in ("noqueue", "plain"))
     model = args.workload in MODEL_WORKLOADS
+    if args.warmup is None:
+        args.warmup = 5 if model else 200
     r = run_model(args, pkg, torch) if model else run_gpu(args, pkg, torch)
     # the CPU oracle covers the layer; a CPU training step of the 270M model is not sampled
     cpu = None if (args.no_cpu_baseline or model) else run_cpu_baseline(args, torch)
