@@ -46,7 +46,7 @@ pytestmark = pytest.mark.gpu
 SCALE = 128 ** -0.5
 
 
-def _inputs(kind, n, H, seed):
+def _inputs(kind, n, H, seed, dt=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
     q, k, v = (torch.randn(1, n, H, 128, generator=g) for _ in range(3))
     t = torch.arange(n, dtype=torch.float32)[None, :, None] / n
@@ -60,7 +60,7 @@ def _inputs(kind, n, H, seed):
         q, k = 16.0 * q, 16.0 * k
     elif kind == "shared":
         k[..., :4] = 32.0
-    return [x.bfloat16() for x in (q, k, v)]
+    return [x.to(dt) for x in (q, k, v)]
 
 
 BLOCK_Q = 256  # queries per block of the dQ kernel
@@ -141,10 +141,10 @@ def test_softmax_edges(pkg, dev, kind, n):
         assert_close(got, r, f"{kind} {name}", max_abs=float("inf"), rel_l2=3e-2)
 
 
-def _dense_case(pkg, dev, kind, n, H):
-    """Device O, lse, dq, dk, dv and the fp32 oracle's (O, lse in log2 units, grads)."""
+def _dense_case(pkg, dev, kind, n, H, dt=torch.bfloat16):
+    """Device O, dq, dk, dv and the fp32 oracle's (O and grads), rows of type dt."""
     N = pkg._native
-    cpu = _inputs(kind, n, H, 7)
+    cpu = _inputs(kind, n, H, 7, dt)
     gpu = [c.to(dev) for c in cpu]
     x = gpu[0]
     rows = N.Rows(*gpu, (x.stride(0), x.stride(1), x.stride(2)))
@@ -152,20 +152,23 @@ def _dense_case(pkg, dev, kind, n, H):
     q, k, v = [c.float().transpose(1, 2).clone().requires_grad_() for c in cpu]
     ref = O.sdpa_causal(q, k, v)
     g = torch.Generator().manual_seed(8)
-    do = torch.randn(1, H, n, 128, generator=g).bfloat16()
+    do = torch.randn(1, H, n, 128, generator=g).to(dt)
     ref.backward(do.float())
-    delta = (do.float() * o.float().cpu()).sum(-1)  # from the bf16 O, as the layer forms it
+    delta = (do.float() * o.float().cpu()).sum(-1)  # from the rounded O, as the layer forms it
     dq, dk, dv = N.attn_bwd(rows, None, 1, H, n, do.to(dev), lse, delta.to(dev))
     return (o, dq, dk, dv), (ref, q.grad, k.grad, v.grad)
 
 
-def test_shared_key_channels(pkg, dev):
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_shared_key_channels(pkg, dev, dt):
     """Four key channels constant (32) over all keys: standard tolerance for O and
-    every gradient (without the key centring, dQ misses it: max-abs 2.1x the
-    bound, rel-L2 1.5e-2 in a CPU emulation of the kernel's roundings)."""
+    every gradient (without the key centring, dQ misses it in bf16: max-abs 2.1x
+    the bound, rel-L2 1.5e-2 in a CPU emulation of the kernel's roundings); fp16
+    rows take the same centring path."""
     n, H = 1500, 2
-    print(f"softmax edges shared n={n}", flush=True)
-    got, ref = _dense_case(pkg, dev, "shared", n, H)
+    print(f"softmax edges shared n={n} {dt}", flush=True)
+    got, ref = _dense_case(pkg, dev, "shared", n, H, dt)
+    assert all(a.dtype == dt for a in got)
     for name, a, r in zip(("out", "dq", "dk", "dv"), got, ref):
         assert_close(a, r, f"shared {name}")
 
