@@ -40,7 +40,7 @@ extern "C" {
 #define LH_ERR_RUNTIME 5      /* a HIP runtime call (synchronize, copy, symbol lookup) failed */
 
 /* The ABI this header declares; lh_abi_version() of a matching library returns it. */
-#define LH_ABI_VERSION 8
+#define LH_ABI_VERSION 9
 
 #define LH_DTYPE_BF16 0       /* row element type: bfloat16 (the reference configs) */
 #define LH_DTYPE_F16 1        /* row element type: IEEE half */
@@ -81,7 +81,7 @@ int lh_select_geometry(int S, int L, int p, int topk, int strict,
  *     lh_gla_scores) and only the max-pooled levels are made.
  * Every row-reading entry point of this library below takes the same dtype
  * argument (its rows, outputs and rounding follow it; sums are fp32);
- * the rotary and GLA entry points are bf16 only.
+ * the rotary entry points are bf16 only.
  */
 int lh_pyramid_fwd(const void *xq, const void *xk, const void *xv,
                    int64_t sb, int64_t ss, int64_t sh,
@@ -130,13 +130,14 @@ int lh_dilated_scores(const void *xq, const void *xk, const void *xv,
                       void *stream);
 
 /*
- * GLA scorer base scores: the bf16-rounded L2 norms of the two simple gated
- * linear attention outputs o = chunk_simple_gla(q, k, v, g, scale) and
- * chunk_simple_gla(k, q, v, g, scale) (each output rounded to bf16 first) over
- * the dilated virtual heads, written to scores_qk/_kq[:, :, 0:S].
+ * GLA scorer base scores: the L2 norms of the two simple gated linear
+ * attention outputs o = chunk_simple_gla(q, k, v, g, scale) and
+ * chunk_simple_gla(k, q, v, g, scale) over the dilated virtual heads (each
+ * output rounded to dtype first, the norm rounded to dtype), written to
+ * scores_qk/_kq[:, :, 0:S].
  * Replaces the two fla chunk_simple_gla calls and norms of
  * DilatedLighthouseGLAScorer.forward (src/lighthouse_selection.py:713-734).
- *   xq, xk, xv  bf16 [B, S, H, D] contiguous; gk fp32 [B, S, H] contiguous log gates
+ *   xq, xk, xv  dtype [B, S, H, D] contiguous; gk fp32 [B, S, H] contiguous log gates
  *   (token t of head h is position t / dilation of virtual head (t % dilation) * H + h)
  *   segments   <= 0: automatic, one per 32 chunks of 64 tokens (at least one),
  *              from the per-sequence length S / dilation alone, so a sequence's
@@ -145,7 +146,7 @@ int lh_dilated_scores(const void *xq, const void *xk, const void *xv,
  *              the 64-token chunk count).  Segment s starts
  *              from the combined final states of segments 0..s-1, which a first
  *              pass computes; results agree with the one-segment walk to fp32
- *              rounding of the state (the bf16 scores may differ in the last bit).
+ *              rounding of the state (the rounded scores may differ in the last bit).
  *   workspace  device buffer of lh_gla_workspace_bytes(...) bytes (16-byte aligned),
  *              may be NULL when that size is 0; workspace_bytes is its size.
  * Then lh_pyramid_fwd with base_scores_given = 1 pools the levels.
@@ -153,7 +154,7 @@ int lh_dilated_scores(const void *xq, const void *xk, const void *xv,
 int lh_gla_scores(const void *xq, const void *xk, const void *xv, const float *gk,
                   float *scores_qk, float *scores_kq,
                   int B, int S, int H, int D, int dilation, int S_tot, float scale,
-                  int segments, void *workspace, int64_t workspace_bytes, void *stream);
+                  int segments, void *workspace, int64_t workspace_bytes, int dtype, void *stream);
 
 /*
  * Workspace bytes lh_gla_scores needs for this geometry and `segments` (0 when

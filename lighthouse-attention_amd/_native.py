@@ -39,7 +39,7 @@ _SIGS = {
     "lh_pyramid_fwd": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _P, _L, _L, _L, _P, _P,
                             _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_dilated_scores": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P]),
-    "lh_gla_scores": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _L, _P]),
+    "lh_gla_scores": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _L, _I, _P]),
     "lh_gla_workspace_bytes": (_L, [_I, _I, _I, _I, _I, _I]),
     "lh_select_topk": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "lh_build_inverse": (_I, [_P, _I, _P, _I, _I, _I, _P]),
@@ -311,8 +311,9 @@ def gla_scores(xq, xk, xv, gk, dilation: int, S_tot: int, scale: float | None = 
     """Base-level GLA scores into fresh fp32 [B, H, S_tot] buffers (pooled levels unset).
     ``gk`` [B, S, H] log gates (any float dtype; taken in fp32, as fla does).
     ``segments``: sequence segments walked in parallel (0: chosen from the
-    geometry so that every CU gets a workgroup; 1: one sequential walk)."""
-    _need_rows("gla_scores", xq, xk, xv, dtypes=BF16_ONLY)
+    sequence length alone; 1: one sequential walk).  Rows bf16 or fp16; the
+    scores are rounded to the row type."""
+    dt = _need_rows("gla_scores", xq, xk, xv)
     _need_gpu(xq, xk, xv, gk)
     B, S, H, D = xq.shape
     for t in (xq, xk, xv):
@@ -330,7 +331,7 @@ def gla_scores(xq, xk, xv, gk, dilation: int, S_tot: int, scale: float | None = 
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev) if nbytes else None
     with torch.cuda.device(dev):
         rc = lib().lh_gla_scores(_ptr(xq), _ptr(xk), _ptr(xv), _ptr(g), _ptr(sqk), _ptr(skq), B, S, H, D, dilation,
-                                 S_tot, float(scale), int(segments), _ptr(ws), nbytes,
+                                 S_tot, float(scale), int(segments), _ptr(ws), nbytes, dt,
                                  _stream(dev))
     _check(rc, "lh_gla_scores")
     return sqk, skq

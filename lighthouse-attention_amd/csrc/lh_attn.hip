@@ -1472,7 +1472,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
 // ===========================================================================
 // GLA scorer: simple gated linear attention over the dilated virtual heads,
 //   o_t = scale * sum_{s <= t} exp(G_t - G_s) (q_t . k_s) v_s,  G = cumsum(g),
-// and the bf16-rounded L2 norm of the bf16-rounded o_t as the base score.
+// and the L2 norm of o_t rounded to the row type (bf16 or fp16), itself
+// rounded to that type, as the base score.
 // Chunked form (chunks of 64 tokens, processed in order): with b the
 // chunk-local inclusive cumsum of g and H the state after the previous chunk,
 //   o = scale * ((Q K^T) o exp(b_t - b_s), causal) V + scale * exp(b_t) Q H
@@ -1488,13 +1489,14 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv_kernel(const AttnArgs a,
 // One workgroup (8 waves) owns one segment of one (b, virtual head,
 // direction).  The state is kept transposed, H^T [j][i] (j: value dim, i: key
 // dim), in fp32 MFMA accumulators (wave w: rows 32 (w >> 1), columns 64 (w & 1)
-// .. + 63) with a bf16 copy in LDS as the operand of the inter-chunk product.
+// .. + 63) with a copy rounded to the row type in LDS as the operand of the
+// inter-chunk product (fp16 rows: fp16 MFMAs, an fp16 state copy).
 // As in the forward kernel, products come out transposed (A^T, O^T), so an
 // accumulator column is a token.  Per chunk: phase 1 (waves 0-2) forms the
-// three causal 32x32 blocks of A^T and hands them over in LDS as packed bf16
+// three causal 32x32 blocks of A^T and hands them over in LDS as packed
 // operands, wave 3 the decay factors; phase 2 every wave forms one 32-token x
 // 32-column block of O^T (norm partials to LDS) and updates its state blocks;
-// phase 3 writes the new bf16 state copy and wave 7 finishes the norms.  Tiles
+// phase 3 writes the new state copy and wave 7 finishes the norms.  Tiles
 // of the next chunk are loaded (direct global->LDS) during the current one.
 // ===========================================================================
 struct GlaArgs {
@@ -1587,6 +1589,7 @@ __device__ __forceinline__ void gla_decays(float x, int nvalid, int lane, float*
 }
 
 // H^T <- exp(b_last) H^T + (V o f)^T K for this wave's two state blocks
+template <typename T>
 __device__ __forceinline__ void gla_state_update(floatx16 (&hs)[2], float el, const bf16_t* Vt, const bf16_t* Kt,
                                                  const float* Fs, const LaneLds& ll, int sjb, int sib, int hh) {
 #pragma unroll
@@ -1599,16 +1602,17 @@ __device__ __forceinline__ void gla_state_update(floatx16 (&hs)[2], float el, co
     const float fv[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float lo = __uint_as_float(vt[e] << 16) * fv[2 * e];
-      const float hi = __uint_as_float(vt[e] & 0xffff0000u) * fv[2 * e + 1];
-      vt[e] = cvt2<BF16>(lo, hi);
+      const float lo = T::lo(vt[e]) * fv[2 * e];
+      const float hi = T::hi(vt[e]) * fv[2 * e + 1];
+      vt[e] = cvt2<T>(lo, hi);
     }
 #pragma unroll
-    for (int q = 0; q < 2; ++q) hs[q] = mfma<BF16>(vt, lds_tr(Kt, ll, 16 * kk, sib + q), hs[q]);
+    for (int q = 0; q < 2; ++q) hs[q] = mfma<T>(vt, lds_tr(Kt, ll, 16 * kk, sib + q), hs[q]);
   }
 }
 
-// bf16 copy of this wave's state blocks into the LDS operand H^T
+// Copy of this wave's state blocks, rounded to the element type, into the LDS operand H^T
+template <typename T>
 __device__ __forceinline__ void gla_state_copy(bf16_t (*HT)[TILE], const floatx16 (&hs)[2], int sjb, int sib,
                                                int l32, int hh) {
 #pragma unroll
@@ -1617,15 +1621,17 @@ __device__ __forceinline__ void gla_state_copy(bf16_t (*HT)[TILE], const floatx1
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int j = 32 * sjb + slot_key(v, hh);
-      HT[j >> 6][tile_elem(j & 63, i)] = (bf16_t)(cvt2<BF16>(hs[q][v], 0.f) & 0xffffu);
+      HT[j >> 6][tile_elem(j & 63, i)] = (bf16_t)(cvt2<T>(hs[q][v], 0.f) & 0xffffu);
     }
   }
 }
 
-// State pass: segment s < P - 1 of a sequence, from a zero state, K / V / g
-// tiles only; stores the final fp32 state blocks and the segment's decay.
+// State pass (E: the row element type): segment s < P - 1 of a sequence,
+// from a zero state, K / V / g tiles only; stores the final fp32 state blocks
+// and the segment's decay.
 // Every wave forms the chunk's decay factors itself (in a wave-private LDS
 // row), so one barrier per chunk (tile reuse) suffices.
+template <typename E>
 __global__ __launch_bounds__(512, 1) void gla_state_kernel(const GlaArgs a) {
   __shared__ __attribute__((aligned(1024))) bf16_t Kt[2][TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t Vt[2][TILE];
@@ -1660,7 +1666,7 @@ __global__ __launch_bounds__(512, 1) void gla_state_kernel(const GlaArgs a) {
     Fw[w][lane] = lane < nvalid ? ex2(bl - x) : 0.f;
     const float el = ex2(bl);
     dec *= el;
-    gla_state_update(hs, el, Vt[buf], Kt[buf], Fw[w], ll, sjb, sib, hh);
+    gla_state_update<E>(hs, el, Vt[buf], Kt[buf], Fw[w], ll, sjb, sib, hh);
     wait_loads();
     __syncthreads();
   }
@@ -1685,6 +1691,7 @@ __global__ __launch_bounds__(512, 1) void gla_state_kernel(const GlaArgs a) {
 // Tiles of chunk c + 2 are issued at the start of phase B of chunk c, into the
 // buffers chunk c has just released, and waited for at the end of phase A of
 // chunk c + 1.
+template <typename E>
 __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
   __shared__ __attribute__((aligned(1024))) bf16_t Qt[2][TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t Kt[2][TILE];
@@ -1720,7 +1727,7 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
       }
     }
   }
-  gla_state_copy(HT, hs, sjb, sib, l32, hh);
+  gla_state_copy<E>(HT, hs, sjb, sib, l32, hh);
 
   auto issue = [&](int c, int buf) {
     const int t0 = 64 * c;
@@ -1742,7 +1749,7 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
     const int tb = w == 0 ? 0 : 1, sbk = w == 2 ? 1 : 0;
     floatx16 acc = floatx16{};
 #pragma unroll
-    for (int cc = 0; cc < 8; ++cc) acc = mfma<BF16>(lds_row(Kt[buf], ll, sbk, cc), lds_row(Qt[buf], ll, tb, cc), acc);
+    for (int cc = 0; cc < 8; ++cc) acc = mfma<E>(lds_row(Kt[buf], ll, sbk, cc), lds_row(Qt[buf], ll, tb, cc), acc);
     const int t = 32 * tb + l32;
     const float bt = Bw[w][t];
 #pragma unroll
@@ -1756,8 +1763,8 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
         acc[v] = (s <= t && s < nvalid) ? acc[v] * a.scale * ex2(bt - b4[r]) : 0.f;
       }
     }
-    AP[buf][w][0][lane] = pack_frag<BF16>(acc, 0);
-    AP[buf][w][1][lane] = pack_frag<BF16>(acc, 1);
+    AP[buf][w][0][lane] = pack_frag<E>(acc, 0);
+    AP[buf][w][1][lane] = pack_frag<E>(acc, 1);
   };
 
   issue(c0, 0);
@@ -1776,7 +1783,7 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
       // inter-chunk: H^T rows of column block odb against the chunk's queries
 #pragma unroll
       for (int cc = 0; cc < 8; ++cc)
-        oi = mfma<BF16>(lds_row(HT[odb >> 1], ll, odb & 1, cc), lds_row(Qt[buf], ll, otb, cc), oi);
+        oi = mfma<E>(lds_row(HT[odb >> 1], ll, odb & 1, cc), lds_row(Qt[buf], ll, otb, cc), oi);
       // intra-chunk: V^T against the packed A^T blocks of this token block
 #pragma unroll
       for (int sbk = 0; sbk < 2; ++sbk) {
@@ -1784,29 +1791,28 @@ __global__ __launch_bounds__(512, 1) void gla_scores_kernel(const GlaArgs a) {
         const int blk = otb == 0 ? 0 : 1 + sbk;
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2)
-          oa = mfma<BF16>(lds_tr(Vt[buf], ll, 32 * sbk + 16 * c2, odb), AP[buf][blk][c2][lane], oa);
+          oa = mfma<E>(lds_tr(Vt[buf], ll, 32 * sbk + 16 * c2, odb), AP[buf][blk][c2][lane], oa);
       }
       const float et = Es[buf][32 * otb + l32] * a.scale;
       float ss = 0.f;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const float o = fmaf(oi[v], et, oa[v]);
-        const float ob = __uint_as_float(cvt2<BF16>(o, 0.f) << 16);  // the bf16 output value
+        const float ob = round_to<E>(o);  // the output value as stored in the row type
         ss = fmaf(ob, ob, ss);
       }
       ss += __shfl_xor(ss, 32);
       if (hh == 0) RED[odb][32 * otb + l32] = ss;
-      gla_state_update(hs, Es[buf][nvalid - 1], Vt[buf], Kt[buf], Fs[buf], ll, sjb, sib, hh);
+      gla_state_update<E>(hs, Es[buf][nvalid - 1], Vt[buf], Kt[buf], Fs[buf], ll, sjb, sib, hh);
     }
     wait_loads();  // tiles of chunk c + 1
     __syncthreads();
-    // ---- phase B: bf16 copy of the new state; norms of chunk c; A^T and decays of chunk c + 1
+    // ---- phase B: rounded copy of the new state; norms of chunk c; A^T and decays of chunk c + 1
     if (c + 2 < c1) issue(c + 2, buf);
-    gla_state_copy(HT, hs, sjb, sib, l32, hh);
+    gla_state_copy<E>(HT, hs, sjb, sib, l32, hh);
     if (w == 7 && lane < nvalid) {
       const float ss = (RED[0][lane] + RED[1][lane]) + (RED[2][lane] + RED[3][lane]);
-      const uint32_t nb = cvt2<BF16>(sqrtf(ss), 0.f) << 16;
-      sq.scores[(int64_t)(64 * c + lane) * a.dil] = __uint_as_float(nb);
+      sq.scores[(int64_t)(64 * c + lane) * a.dil] = round_to<E>(sqrtf(ss));
     }
     if (c + 1 < c1) prep(c + 1, buf ^ 1);
     __syncthreads();
@@ -2243,9 +2249,10 @@ extern "C" int64_t lh_gla_workspace_bytes(int B, int S, int H, int D, int dilati
 
 extern "C" int lh_gla_scores(const void* xq, const void* xk, const void* xv, const float* gk, float* scores_qk,
                              float* scores_kq, int B, int S, int H, int D, int dilation, int S_tot, float scale,
-                             int segments, void* workspace, int64_t workspace_bytes, void* stream) {
+                             int segments, void* workspace, int64_t workspace_bytes, int dtype, void* stream) {
   int rc = gla_check(xq, xk, xv, gk, B, S, H, D, dilation, scale);
   if (rc) return rc;
+  if (!valid_dtype(dtype)) return LH_ERR_INVALID_ARG;
   if (!scores_qk || !scores_kq || S_tot < S) return LH_ERR_INVALID_ARG;
   GlaArgs a{};
   a.q = (const bf16_t*)xq; a.k = (const bf16_t*)xk; a.v = (const bf16_t*)xv; a.g = gk;
@@ -2260,11 +2267,10 @@ extern "C" int lh_gla_scores(const void* xq, const void* xk, const void* xv, con
     a.ws = (float*)workspace;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (a.P > 1) {
-    hipLaunchKernelGGL(gla_state_kernel, dim3((unsigned)(units * (a.P - 1))), dim3(512), 0, st, a);
-    LH_CHECK_LAUNCH();
-  }
-  hipLaunchKernelGGL(gla_scores_kernel, dim3((unsigned)(units * a.P)), dim3(512), 0, st, a);
+  LH_DISPATCH_DTYPE(dtype, {
+    if (a.P > 1) hipLaunchKernelGGL(gla_state_kernel<T>, dim3((unsigned)(units * (a.P - 1))), dim3(512), 0, st, a);
+    hipLaunchKernelGGL(gla_scores_kernel<T>, dim3((unsigned)(units * a.P)), dim3(512), 0, st, a);
+  });
   LH_CHECK_LAUNCH();
   return LH_OK;
 }

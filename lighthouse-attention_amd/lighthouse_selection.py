@@ -272,8 +272,6 @@ def lighthouse_layer(xq, xk, xv, num_levels: int = 3, pooling_factor: int = 4, t
     if gk is not None:
         if dilation <= 0:
             raise ValueError("the GLA scorer needs dilation >= 1")
-        if xq.dtype != torch.bfloat16:
-            raise TypeError("the GLA scorer's kernels read bfloat16 rows; got " + str(xq.dtype))
         gk = gk.detach()
     scale = None
     if D < N.D_SUPPORTED:

@@ -521,7 +521,7 @@ def simple_gla_recurrent(q, k, v, g, scale: float):
 
 
 def gla_scorer(xq, xk, xv, gk, dilation: int = 4, pooling_factor: int = 4, levels: int = 3,
-               scale: float | None = None, round_bf16: bool = False):
+               scale: float | None = None, round_bf16: bool = False, round_to=None):
     """``DilatedLighthouseGLAScorer.forward`` (``src/lighthouse_selection.py:713-755``).
 
     Token t of head h is position ``t // dil`` of virtual head ``(t % dil) * H + h``
@@ -530,7 +530,10 @@ def gla_scorer(xq, xk, xv, gk, dilation: int = 4, pooling_factor: int = 4, level
     with v and the gate ``gk`` [B, S, H] viewed the same way (:727-734).  The Q/K/V
     pyramid and the max-pooled score levels are the norm scorer's (:736-755).
     ``round_bf16`` rounds the GLA outputs to bfloat16 before the norm and the norm
-    after it, as the reference's bf16 tensors do."""
+    after it, as the reference's bf16 tensors do; ``round_to`` (a torch dtype)
+    does the same for another 16-bit type."""
+    if round_bf16:
+        round_to = torch.bfloat16
     b, s, h, d = xq.shape
     sd = s // dilation
     scale = d ** -0.5 if scale is None else scale
@@ -542,12 +545,12 @@ def gla_scorer(xq, xk, xv, gk, dilation: int = 4, pooling_factor: int = 4, level
     with torch.no_grad():
         o_qk = simple_gla(virt(xq), virt(xk), virt(xv), g, scale).reshape(b, s, h, d)
         o_kq = simple_gla(virt(xk), virt(xq), virt(xv), g, scale).reshape(b, s, h, d)
-        if round_bf16:
-            o_qk, o_kq = o_qk.bfloat16().double(), o_kq.bfloat16().double()
+        if round_to is not None:
+            o_qk, o_kq = o_qk.to(round_to).double(), o_kq.to(round_to).double()
         sqk = torch.linalg.vector_norm(o_qk, dim=-1).float()
         skq = torch.linalg.vector_norm(o_kq, dim=-1).float()
-        if round_bf16:
-            sqk, skq = sqk.bfloat16().float(), skq.bfloat16().float()
+        if round_to is not None:
+            sqk, skq = sqk.to(round_to).float(), skq.to(round_to).float()
     ql, kl, vl, al, bl = [xq], [xk], [xv], [sqk], [skq]
     for level in range(1, levels):
         pf = pooling_factor ** level

@@ -237,15 +237,15 @@ def test_row_kernels_refuse_non_bf16(pkg):
         N.Rows(xb.transpose(-1, -2), xb, xb, (0, 0, 0))
 
 
-def test_layer_refuses_float32_and_fp16_gla(pkg):
-    """Float32 inputs are refused rather than silently downcast, and the GLA
-    scorer (bf16 kernels only) refuses fp16, all before any device work."""
+def test_layer_refuses_float32_and_mixed_dtypes(pkg):
+    """Float32 inputs are refused rather than silently downcast, and so are
+    inputs of different dtypes, before any device work."""
     x = torch.zeros(1, 512, 2, 128)
     with pytest.raises(TypeError, match="bfloat16 or float16"):
         pkg.lighthouse_layer(x, x, x, num_levels=3, pooling_factor=4, topk=128)
     h = x.half()
     with pytest.raises(TypeError, match="share a dtype"):
         pkg.lighthouse_layer(h, h.bfloat16(), h, num_levels=3, pooling_factor=4, topk=128)
-    with pytest.raises(TypeError, match="GLA"):
-        pkg.lighthouse_layer(h, h, h, num_levels=3, pooling_factor=4, topk=128, dilation=4,
+    with pytest.raises(TypeError, match="bfloat16 or float16"):
+        pkg.lighthouse_layer(x, x, x, num_levels=3, pooling_factor=4, topk=128, dilation=4,
                              gk=torch.zeros(1, 512, 2))

@@ -58,6 +58,67 @@ def test_gla_scores(pkg, dev, B, S, H, dil, gate):
         assert (_ulps(got, ref) <= 1).float().mean().item() >= 0.95, f"{name}: fewer than 95% within 1 ulp"
 
 
+def _inputs_f16(B, S, H, gate, seed, dev):
+    xs, gk, _, _ = _inputs(B, S, H, gate, seed, dev)
+    g = torch.Generator().manual_seed(seed)
+    xs = [torch.randn(B, S, H, D, generator=g).half() for _ in range(3)]
+    return xs, gk, [x.to(dev) for x in xs], gk.to(dev)
+
+
+def _ulps16(a, b, mant):
+    a, b = a.float(), b.float()
+    ulp = torch.pow(2.0, torch.floor(torch.log2(b.abs().clamp_min(1e-30))) - mant)
+    return (a - b).abs() / ulp
+
+
+@pytest.mark.parametrize("B,S,H,dil,gate,segs", [(1, 1024, 2, 4, "typical", 0), (2, 1000, 1, 4, "strong", 0),
+                                                 (1, 8192, 1, 2, "none", 3), (1, 16384, 1, 4, "typical", 0)])
+def test_gla_scores_fp16(pkg, dev, B, S, H, dil, gate, segs):
+    """fp16 rows: fp16 MFMAs and an fp16 state copy; outputs and norms rounded to
+    fp16, against the float64 oracle with the same roundings (standard tolerance,
+    at least 90% within one fp16 ulp)."""
+    print(f"gla scores fp16 B={B} S={S} H={H} dil={dil} gate={gate} segments={segs}", flush=True)
+    N = pkg._native
+    L, p = 3, 2
+    xs, gk, xd, gd = _inputs_f16(B, S, H, gate, S + H + 1, dev)
+    _, _, S_tot = N.pyramid_lengths(S, L, p)
+    sqk, skq = N.gla_scores(*xd, gd, dil, S_tot, segments=segs)
+    r_qk, r_kq, *_ = O.gla_scorer(*[x.float() for x in xs], gk.float(), dil, p, L, round_to=torch.float16)
+    for got, ref, name in ((sqk, r_qk, "qk"), (skq, r_kq, "kq")):
+        got = got[..., :S].cpu()
+        ref = ref[..., :S]
+        assert torch.equal(got, got.half().float()), f"{name}: scores are not fp16 values"
+        assert_close(got, ref, f"gla fp16 scores {name}")
+        assert (_ulps16(got, ref, 10) <= 1).float().mean().item() >= 0.90, f"{name}: fewer than 90% within 1 ulp"
+
+
+def test_gla_layer_fp16(pkg, dev):
+    """The layer with the GLA scorer on fp16 rows: indices bit-exact on the
+    device's own scores, outputs and gradients (fp16) against the fp32 oracle on
+    that index set."""
+    N = pkg._native
+    B, S, H, L, p, k, dil = 1, 4096, 2, 3, 4, 256, 4
+    print(f"gla layer fp16 S={S} H={H} k={k} dil={dil}", flush=True)
+    xs, gk, xd, gd = _inputs_f16(B, S, H, "typical", 12, dev)
+    xg = [x.clone().requires_grad_() for x in xd]
+    out, idx = pkg.lighthouse_layer(*xg, num_levels=L, pooling_factor=p, topk=k, dilation=dil, gk=gd)
+    assert out.dtype == torch.float16
+    do = torch.randn(out.shape, generator=torch.Generator().manual_seed(3)).half()
+    out.backward(do.to(dev))
+    _, _, S_tot = N.pyramid_lengths(S, L, p)
+    sc = N.gla_scores(*xd, gd, dil, S_tot)
+    _, _, _, sqk, skq = N.pyramid_fwd(*xd, L, p, scores=sc)
+    ref_idx = R.select_indices_c(sqk.cpu().numpy(), skq.cpu().numpy(), L, p, k, S, idx.shape[-1])
+    assert np.array_equal(idx.cpu().numpy(), ref_idx)
+    xc = [x.float().requires_grad_() for x in xs]
+    ref, _ = O.lighthouse_layer(*xc, L, p, k, scorer="gla", dilation=dil, gk=gk.float(), indices=ref_idx)
+    ref.backward(do.float())
+    assert_close(out, ref, "gla fp16 layer out")
+    for n_, x, c in zip("qkv", xg, xc):
+        assert x.grad.dtype == torch.float16
+        assert_close(x.grad, c.grad, f"gla fp16 layer d{n_}")
+
+
 def test_gla_layer_against_oracle(pkg, dev):
     """LighthouseLocal with the GLA scorer: selection bit-exact on the device's own
     scores (C restatement), outputs and gradients against the fp32 oracle on that
@@ -160,9 +221,9 @@ def test_gla_workspace_errors(pkg, dev):
     ptr = N._ptr
     args = [ptr(xd[0]), ptr(xd[1]), ptr(xd[2]), ptr(gd.float().contiguous()), ptr(out[0]), ptr(out[1]),
             B, S, H, D, dil, S, 1.0 / D ** 0.5, 4]
-    assert lib.lh_gla_scores(*args, None, 0, N._stream(dev)) == 1  # LH_ERR_INVALID_ARG
-    assert lib.lh_gla_scores(*args, ptr(ws), need - 4, N._stream(dev)) == 1  # LH_ERR_INVALID_ARG
-    assert lib.lh_gla_scores(*args, ptr(ws), need, N._stream(dev)) == 0
+    assert lib.lh_gla_scores(*args, None, 0, 0, N._stream(dev)) == 1  # LH_ERR_INVALID_ARG
+    assert lib.lh_gla_scores(*args, ptr(ws), need - 4, 0, N._stream(dev)) == 1  # LH_ERR_INVALID_ARG
+    assert lib.lh_gla_scores(*args, ptr(ws), need, 0, N._stream(dev)) == 0
     torch.cuda.synchronize()
 
 
