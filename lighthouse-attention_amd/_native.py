@@ -160,7 +160,8 @@ def _need_dtype(what, dtype, *ts):
 
 # Index validation before every launch that reads caller indices: off by default,
 # on with LH_CHECK_INDICES=1 in the environment or set_check_indices(True).  Each
-# check synchronizes the stream (debug aid, not for timed runs).
+# check synchronizes the stream (debug aid, not for timed runs), so the checks
+# are skipped while the current stream is being captured into a graph.
 _check_indices = os.environ.get("LH_CHECK_INDICES", "0") not in ("", "0")
 
 
@@ -368,7 +369,7 @@ def build_inverse(indices, S_tot: int, validate: bool = False):
     the indices are first checked to lie in [0, S_tot) and be unique per (b, h)."""
     _need_dtype("build_inverse indices", torch.int32, indices)
     _need_gpu(indices)
-    if validate or _check_indices:
+    if validate or _check_mode():
         check_indices(indices, 0, S_tot, unique=True, what="indices")
     idx = indices.contiguous()
     B, H, n = idx.shape
@@ -406,9 +407,14 @@ def set_attention_schedule(plans: bool = True, queues: bool = True):
     return (not prev.value & SCHED_NO_PLAN, not prev.value & SCHED_NO_QUEUE)
 
 
+def _check_mode() -> bool:
+    """Check mode is on and the current stream can synchronize (not capturing)."""
+    return _check_indices and torch.cuda.is_available() and not torch.cuda.is_current_stream_capturing()
+
+
 def _check_queues(dev, what: str):
     """In check mode, raise if an attention launch found its work-queue counters dirty."""
-    if _check_indices:
+    if _check_mode():
         n = attn_status(dev)
         if n:
             raise LighthouseHipError(
@@ -433,7 +439,7 @@ class Rows:
         self.limit = int(limit) if limit is not None else None
 
     def check(self, indices):
-        if _check_indices and indices is not None and self.limit is not None:
+        if _check_mode() and indices is not None and self.limit is not None:
             check_indices(indices, 0, self.limit, unique=False, what="attention row indices")
 
     def args(self):
@@ -530,7 +536,7 @@ def scatter_fwd(attn, inverse, S: int, S_out: int, L: int, p: int, seq_major: bo
     _need_gpu(attn, inverse)
     attn = attn.contiguous()
     B, H, n, D = attn.shape
-    if _check_indices:
+    if _check_mode():
         check_indices(inverse, -1, n, unique=False, what="scatter_fwd inverse map")
     if seq_major:
         out = torch.empty(B, S_out, H, D, dtype=attn.dtype, device=attn.device).transpose(1, 2)
@@ -550,7 +556,7 @@ def scatter_bwd(dout, indices, o, S: int, L: int, p: int):
     dt = _need_rows("scatter_bwd", dout, o)
     _need_dtype("scatter_bwd indices", torch.int32, indices)
     _need_gpu(dout, indices, o)
-    if _check_indices:
+    if _check_mode():
         check_indices(indices, 0, pyramid_lengths(S, L, p)[2], unique=True, what="scatter_bwd indices")
     if dout.stride(3) != 1 or any(st % 8 for st in dout.stride()[:3]) or dout.data_ptr() % 16:
         dout = dout.contiguous()
@@ -574,7 +580,7 @@ def pyramid_bwd(gq, gk, gv, inverse, B: int, S: int, H: int, L: int, p: int, D: 
     _need_dtype("pyramid_bwd inverse", torch.int32, inverse)
     ref = next(g for g in (gq, gk, gv) if g is not None)
     _need_gpu(ref, inverse)
-    if _check_indices and inverse is not None:
+    if _check_mode() and inverse is not None:
         check_indices(inverse, -1, ref.shape[2], unique=False, what="pyramid_bwd inverse map")
     dev = ref.device
     outs = [torch.empty(B, S, H, D, dtype=ref.dtype, device=dev) if g is not None else None
