@@ -366,11 +366,12 @@ def select_topk(scores_qk, scores_kq, S: int, L: int, p: int, topk: int, tie: st
 
 def build_inverse(indices, S_tot: int, validate: bool = False):
     """Inverse map of ``indices`` [B, H, n]; with ``validate`` (or the check mode)
-    the indices are first checked to lie in [0, S_tot) and be unique per (b, h)."""
+    the indices are first checked to lie in [0, S_tot) or be -1 (an empty slot,
+    skipped) and to name no row twice per (b, h)."""
     _need_dtype("build_inverse indices", torch.int32, indices)
     _need_gpu(indices)
     if validate or _check_mode():
-        check_indices(indices, 0, S_tot, unique=True, what="indices")
+        check_indices(indices, -1, S_tot, unique=True, what="indices")
     idx = indices.contiguous()
     B, H, n = idx.shape
     inv = torch.empty(B, H, S_tot, dtype=torch.int32, device=idx.device)
