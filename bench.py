@@ -35,7 +35,7 @@ BF16_PEAK_TFLOPS = 2500.0
 MODEL_METRIC = "Llama3 270M Lighthouse training step tokens/s (fwd+bwd+AdamW), S=32K, bf16"
 
 WORKLOADS = {
-    # BASELINE configs 2-4 and the Lighthouse-layer shape of config 5 (config 1 is the CPU-only case).
+    # benchmark configs 2-4 and the Lighthouse-layer shape of config 5 (config 1 is the CPU-only case).
     # heavy_keys: fraction of key positions (the same for every head) scaled by 4, from a seeded draw.
     "cfg2": dict(B=1, H=8, S=32768, L=3, p=4, topk=2048, strict=True, scorer="norm"),
     "cfg3_k1536": dict(B=1, H=8, S=65536, L=3, p=4, topk=1536, strict=False, scorer="norm", heavy_keys=0.05),
@@ -50,7 +50,7 @@ WORKLOADS = {
 D = 128
 # Model workloads: one training step (forward, backward, clip, AdamW) of the Llama3 model.
 MODEL_WORKLOADS = {
-    # the 270M flavor with Lighthouse (norm, L=3, p=4, k=1536) on layers 2-27,
+    # benchmark config 5: the 270M flavor with Lighthouse (norm, L=3, p=4, k=1536) on layers 2-27,
     # dense causal attention on layers 0, 1, 28, 29; byte-level vocabulary; batch 1 x 32768 tokens.
     "cfg5": dict(flavor="ablation_270m_lighthouse_topk1536_pool4_lvl3", B=1, S=32768, vocab=256,
                  layer="cfg5_layer"),

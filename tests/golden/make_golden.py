@@ -2,7 +2,7 @@
 
     python tests/golden/make_golden.py
 
-cfg1_selection.npz     BASELINE config 1: B=1, H=8, D=128, S=4096, fp32 N(0,1) q/k/v
+cfg1_selection.npz     benchmark config 1: B=1, H=8, D=128, S=4096, fp32 N(0,1) q/k/v
                        (torch seed 0), norm scorer, L=3, p=4, topk=1536 (outside the
                        reference kernel's domain, so per-tile compaction); scores and
                        the selected-index dump for both tie modes.

@@ -1,4 +1,4 @@
-"""BASELINE config 5 at its own size: the 270M Llama3 Lighthouse model
+"""Benchmark config 5 at its own size: the 270M Llama3 Lighthouse model
 (``ablation_270m_lighthouse_topk1536_pool4_lvl3``, lighthouse-attention.patch:283-296),
 B=1, S=32768, byte vocabulary.
 
