@@ -138,6 +138,9 @@ int lh_dilated_scores(const void *xq, const void *xk, const void *xv,
  * Replaces the two fla chunk_simple_gla calls and norms of
  * DilatedLighthouseGLAScorer.forward (src/lighthouse_selection.py:713-734).
  *   xq, xk, xv  dtype [B, S, H, D] contiguous; gk fp32 [B, S, H] contiguous log gates
+ *               (the running state is fp32; its copy used as the inter-chunk MFMA
+ *               operand is rounded to dtype, so with fp16 a state entry beyond
+ *               fp16's range, 65504, becomes infinite there)
  *   (token t of head h is position t / dilation of virtual head (t % dilation) * H + h)
  *   segments   <= 0: automatic, one per 32 chunks of 64 tokens (at least one),
  *              from the per-sequence length S / dilation alone, so a sequence's
