@@ -27,13 +27,15 @@ constant over the keys exact:
              the cfg2 size.
 In the rising and falling cases the shared component is a ramp, so no single
 c removes it, and in the large case delta's rounding matters where dP - delta
-nearly cancels (its one-hot rows); the standard max-abs bound is not required
-there.  Each gradient element must instead lie within four bf16 half-ulps of
-the terms that make it,
+nearly cancels (its one-hot rows).  Each gradient element must lie within four
+bf16 half-ulps of the terms that make it,
     |dQ - dQ_ref| <= 4 * 2^-9 * scale * (e |K|),  e = |dS| + P (|dP| + rowsum(|dO| |O|))
 (dK alike with e^T |Q|; dV: 4 * 2^-9 * P^T |dO|), plus 1e-3 of the largest
-reference value, with rel-L2 <= 3e-2 overall; an error in the rescaling would
-break this by orders of magnitude.
+reference value; an error in the rescaling would break this by orders of
+magnitude.  On top of that every output and gradient meets the standard
+tolerance, except dQ of the falling ramp, whose max-abs may reach 1.25 times
+the standard bound (measured 1.14 times; rel-L2 5.2e-3, within the standard
+1e-2).
 """
 import pytest
 import torch
@@ -138,7 +140,8 @@ def test_softmax_edges(pkg, dev, kind, n):
         assert torch.isfinite(got).all(), f"{kind} {name}: non-finite values"
         excess = ((got - r).abs() - b - 1e-3 * r.abs().max()).max().item()
         assert excess <= 0, f"{kind} {name}: beyond the rounding bound by {excess:.3e}"
-        assert_close(got, r, f"{kind} {name}", max_abs=float("inf"), rel_l2=3e-2)
+        wide = kind == "falling" and name == "dq"
+        assert_close(got, r, f"{kind} {name}", max_abs=2.5e-2 if wide else 2e-2)
 
 
 def _dense_case(pkg, dev, kind, n, H, dt=torch.bfloat16):
